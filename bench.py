@@ -1,0 +1,304 @@
+"""Benchmark for the MI355X Jade HIP backend (one GPU).
+
+A step is one pass of the hot path over one batch of synthetic input. The
+headline step (`value`) is the FP32 GEMM C = A.B at 4096^3 from BASELINE
+configs[1], inputs from validation::inputs (xorshift32 seeds 0x12345678 /
+0x9abcdef1, U[-1,1)), resident in HBM before timing. The same JSON line
+carries the causal attention config (B4 H32 S4096 D128), the Softmax
+32768x4096 bandwidth case, the six-op MLP block and the rest of the GEMM
+sweep.
+
+Timing follows the reference's jr_execute scope (native/jade_runtime_corex.cpp:
+148-189): W untimed replays, then hipEvents around K ordered launches on the
+runtime's stream (the stream every kernel runs on). `roofline.achieved` is the
+dominant kernel's algorithmic FLOP per launch divided by the event-measured
+average launch time.
+
+The CPU baseline is the reference's own CPU path, its FP64 oracle loops
+(restated in oracle/), timed on this host on a bounded sample; those sampled
+rows also check the GPU output.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "jade-compute_amd"))
+
+import numpy as np  # noqa: E402
+
+import jade_hip  # noqa: E402
+
+METRIC = "FP32 GEMM & attention TFLOP/s (% of MI355X peak), 1 GPU, vs host-CPU ref"
+PEAK_FP32_MFMA_TFLOPS = 157.3
+PEAK_HBM_GBPS = 8000.0
+PROFILE_DIR = os.path.join(ROOT, "profiles")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed(rt, jobs, steps, warmup):
+    if warmup:
+        rt.execute(jobs, warmup)
+    started = time.perf_counter()
+    ex = rt.execute(jobs, steps)
+    wall_ms = (time.perf_counter() - started) * 1000.0
+    if ex.gpu_ms is None:
+        raise RuntimeError("device timer returned no duration")
+    return ex.gpu_ms / steps, wall_ms / steps
+
+
+def traffic_from_profiles(kernel_name):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+    path = os.path.join(PROFILE_DIR, "traffic.json")
+    if not os.path.exists(path):
+        return None
+    try:
+        table = json.load(open(path))
+        return table.get(kernel_name, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_gemm(rt, m, n, k, steps, warmup, keep=False):
+    a = jade_hip.fill_values(m * k, 0x12345678, 1.0)
+    b = jade_hip.fill_values(k * n, 0x9ABCDEF1, 1.0)
+    kernel = rt.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    ag, bg, cg = rt.resident(a), rt.resident(b), rt.alloc(m * n)
+    ms, wall = timed(rt, [(kernel, [ag, bg, cg])], steps, warmup)
+    flops = 2.0 * m * n * k
+    out = {"m": m, "n": n, "k": k, "ms_per_step": ms, "wall_ms_per_step": wall,
+           "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"]}
+    if keep:
+        out["_data"] = (a, b, rt.download(cg))
+    for x in (ag, bg, cg):
+        x.free()
+    return out
+
+
+def bench_attention(rt, heads, seq, dim, causal, steps, warmup, keep=False):
+    n = heads * seq * dim
+    q = jade_hip.fill_normal(n, 0x1111)
+    k = jade_hip.fill_normal(n, 0x2222)
+    v = jade_hip.fill_normal(n, 0x3333)
+    kernel = rt.compile({"op": "attention_online", "heads": heads, "seq": seq, "dim": dim, "causal": causal})
+    bufs = [rt.resident(x) for x in (q, k, v)] + [rt.alloc(n)]
+    ms, wall = timed(rt, [(kernel, bufs)], steps, warmup)
+    keys = seq * (seq + 1) // 2 if causal else seq * seq
+    flops = 4.0 * heads * dim * keys
+    out = {"heads": heads, "seq": seq, "dim": dim, "causal": causal, "flop": flops, "ms_per_step": ms,
+           "wall_ms_per_step": wall, "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"]}
+    if keep:
+        out["_data"] = (q, k, v, rt.download(bufs[3]))
+    for x in bufs:
+        x.free()
+    return out
+
+
+def bench_softmax(rt, rows, cols, steps, warmup):
+    x = jade_hip.fill_normal(rows * cols, 0x6666, 0.0, 2.0)
+    kernel = rt.compile({"op": "softmax", "rows": rows, "cols": cols})
+    xg, og = rt.resident(x), rt.alloc(rows * cols)
+    ms, wall = timed(rt, [(kernel, [xg, og])], steps, warmup)
+    nbytes = 2.0 * rows * cols * 4
+    for b in (xg, og):
+        b.free()
+    return {"rows": rows, "cols": cols, "bytes": nbytes, "ms_per_step": ms, "wall_ms_per_step": wall,
+            "gbps": nbytes / (ms * 1e-3) / 1e9, "kernel": kernel.launch["kernel"]}
+
+
+def bench_mlp(rt, batch, width, hidden, steps, warmup):
+    x = jade_hip.fill_normal(batch * width, 0x1234)
+    gamma = jade_hip.fill_values(width, 0x7777, 0.5) + np.float32(1.0)
+    wg = jade_hip.fill_normal(width * hidden, 0x3333, 0.0, 0.02)
+    wu = jade_hip.fill_normal(width * hidden, 0x4444, 0.0, 0.02)
+    wd = jade_hip.fill_normal(hidden * width, 0x5555, 0.0, 0.02)
+    specs = [
+        ("rms_norm", {"op": "rms_norm", "rows": batch, "cols": width, "epsilon": 1e-6}),
+        ("gemm_gate", {"op": "gemm", "m": batch, "n": hidden, "k": width, "tiled": True}),
+        ("gemm_up", {"op": "gemm", "m": batch, "n": hidden, "k": width, "tiled": True}),
+        ("swiglu", {"op": "swi_glu", "len": batch * hidden}),
+        ("gemm_down", {"op": "gemm", "m": batch, "n": width, "k": hidden, "tiled": True}),
+        ("add", {"op": "add", "len": batch * width}),
+    ]
+    kernels = [rt.compile(s) for _, s in specs]
+    xg, ng, wgg, wug, wdg = (rt.resident(t) for t in (x, gamma, wg, wu, wd))
+    normalized, gate, up = rt.alloc(batch * width), rt.alloc(batch * hidden), rt.alloc(batch * hidden)
+    act, proj, out = rt.alloc(batch * hidden), rt.alloc(batch * width), rt.alloc(batch * width)
+    jobs = [(kernels[0], [xg, ng, normalized]), (kernels[1], [normalized, wgg, gate]),
+            (kernels[2], [normalized, wug, up]), (kernels[3], [gate, up, act]), (kernels[4], [act, wdg, proj]),
+            (kernels[5], [proj, xg, out])]
+    block_ms, block_wall = timed(rt, jobs, steps, warmup)
+    per = {}
+    bw_bytes = {"rms_norm": (2.0 * batch * width + width) * 4, "swiglu": 3.0 * batch * hidden * 4,
+                "add": 3.0 * batch * width * 4}
+    gemm_flops = {"gemm_gate": 2.0 * batch * hidden * width, "gemm_up": 2.0 * batch * hidden * width,
+                  "gemm_down": 2.0 * batch * width * hidden}
+    for (name, _), job in zip(specs, jobs):
+        ms, _ = timed(rt, [job], steps, warmup)
+        entry = {"ms": ms}
+        if name in bw_bytes:
+            entry["gbps"] = bw_bytes[name] / (ms * 1e-3) / 1e9
+            entry["frac_hbm"] = entry["gbps"] / PEAK_HBM_GBPS
+        else:
+            entry["tflops"] = gemm_flops[name] / (ms * 1e-3) / 1e12
+            entry["frac_mfma"] = entry["tflops"] / PEAK_FP32_MFMA_TFLOPS
+        per[name] = entry
+    total_flops = sum(gemm_flops.values())
+    for buf in (xg, ng, wgg, wug, wdg, normalized, gate, up, act, proj, out):
+        buf.free()
+    return {"batch": batch, "width": width, "hidden": hidden, "ms_per_block": block_ms,
+            "wall_ms_per_block": block_wall, "gemm_tflops_block": total_flops / (block_ms * 1e-3) / 1e12,
+            "per_op": per}
+
+
+def cpu_baseline(gemm, attention):
+    """The reference's CPU path (FP64 oracle loops) on this host, bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_binding as orc
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    a, b, c_gpu = gemm["_data"]
+    m, n, k = gemm["m"], gemm["n"], gemm["k"]
+    rows = max(1, min(m, int(os.environ.get("JADE_CPU_ROWS", str(m)))))
+    started = time.perf_counter()
+    ref = orc.gemm_reference(m, n, k, a, b, rows=(0, rows), threads=cores)
+    omp_s = time.perf_counter() - started
+    check = orc.compare(c_gpu[:rows * n], ref, 1e-4, 1e-4)
+    single_rows = max(1, rows // 16)
+    started = time.perf_counter()
+    orc.gemm_reference(m, n, k, a, b, rows=(0, single_rows), threads=1)
+    single_s = time.perf_counter() - started
+    gemm_flop = 2.0 * rows * n * k
+    out = {"value": gemm_flop / omp_s / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+           "sample": f"FP64 gemm_reference (metal_lab.rs:18-31) rows 0..{rows} of the {m}x{n}x{k} GEMM "
+                     f"({gemm_flop:.3e} FLOP, {omp_s:.2f} s on {cores} OpenMP threads)",
+           "single_thread_tflops": 2.0 * single_rows * n * k / single_s / 1e12,
+           "gpu_check_rows": rows, "gpu_check_status": int(check.status),
+           "gpu_max_abs_error": check.max_abs_error, "gpu_max_rel_error": check.max_relative_error}
+    if attention is not None and "_data" in attention:
+        q, kk, v, o_gpu = attention["_data"]
+        h, s, d = attention["heads"], attention["seq"], attention["dim"]
+        r0, r1 = s - 16, s
+        started = time.perf_counter()
+        ref = orc.attention_reference(h, s, d, attention["causal"], q, kk, v, rows=(r0, r1), threads=cores)
+        att_s = time.perf_counter() - started
+        keys = sum(range(r0 + 1, r1 + 1)) if attention["causal"] else (r1 - r0) * s
+        flop = 4.0 * h * d * keys
+        got = o_gpu.reshape(h, s, d)[:, r0:r1].reshape(-1)
+        check = orc.compare(got, ref, 2e-4, 2e-4)
+        out["attention"] = {"value": flop / att_s / 1e12, "unit": "TFLOP/s", "cores": cores,
+                            "sample": f"FP64 attention_reference (metal_lab.rs:33-73) query rows {r0}..{r1} of all "
+                                      f"{h} heads ({flop:.3e} FLOP, {att_s:.2f} s)",
+                            "gpu_check_status": int(check.status), "gpu_max_abs_error": check.max_abs_error}
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.steps <= 0 or args.warmup < 0:
+        sys.exit("steps must be positive and warmup non-negative")
+
+    rt = jade_hip.HipRuntime(0)
+    log(f"device: {rt.device_info}")
+    K, W, wl = args.steps, args.warmup, args.workload
+    extra = {}
+    gemm = attention = None
+    if wl in ("all", "gemm"):
+        log("gemm 4096^3 ...")
+        gemm = bench_gemm(rt, 4096, 4096, 4096, K, W, keep=not args.no_cpu_baseline)
+        log(f"  {gemm['tflops']:.2f} TFLOP/s")
+    if wl in ("all", "attention"):
+        log("attention B4 H32 S4096 D128 causal ...")
+        attention = bench_attention(rt, 128, 4096, 128, True, max(1, K // 4), min(W, 2),
+                                    keep=not args.no_cpu_baseline)
+        log(f"  {attention['tflops']:.2f} TFLOP/s")
+        c3 = {}
+        for causal in (False, True):
+            r = bench_attention(rt, 8, 1024, 64, causal, K, W)
+            c3["causal" if causal else "noncausal"] = {"ms": r["ms_per_step"], "tflops": r["tflops"]}
+        extra["attention_c3_b1h8s1024d64"] = c3
+    if wl in ("all", "softmax"):
+        log("softmax 32768x4096 ...")
+        sm = bench_softmax(rt, 32768, 4096, K, W)
+        sm["frac_hbm"] = sm["gbps"] / PEAK_HBM_GBPS
+        extra["softmax_32768x4096"] = sm
+        log(f"  {sm['gbps']:.0f} GB/s")
+    if wl in ("all", "mlp"):
+        log("six-op MLP 4096x1024x2816 ...")
+        extra["mlp_4096x1024x2816"] = bench_mlp(rt, 4096, 1024, 2816, K, W)
+    if wl in ("all", "sweep"):
+        sweep = {}
+        for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
+                        (4096, 11008, 4096)):
+            r = bench_gemm(rt, m, n, k, K if m * n * k < 1 << 36 else max(2, K // 2), W)
+            sweep[f"{m}x{n}x{k}"] = {"ms": r["ms_per_step"], "tflops": r["tflops"],
+                                     "frac_mfma": r["tflops"] / PEAK_FP32_MFMA_TFLOPS}
+        extra["gemm_sweep"] = sweep
+
+    head = gemm or attention
+    if head is None:
+        head_name = "softmax" if wl == "softmax" else "mlp"
+        print(json.dumps({"metric": METRIC, "workload": head_name, "extra": extra}))
+        return
+    if gemm is not None:
+        flop_per_launch = 2.0 * gemm["m"] * gemm["n"] * gemm["k"]
+        config = {"workload": "FP32 GEMM C=A.B 4096x4096x4096, row-major (BASELINE configs[1] headline)",
+                  "m": 4096, "n": 4096, "k": 4096,
+                  "inputs": "validation::inputs xorshift32 seeds 0x12345678/0x9abcdef1, U[-1,1)"}
+    else:
+        flop_per_launch = attention["flop"]
+        config = {"workload": "FP32 causal attention B4 H32 S4096 D128 (BASELINE configs[4])"}
+    achieved = flop_per_launch / (head["ms_per_step"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": head["tflops"],
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": config,
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
+                     "traffic": traffic_from_profiles(head["kernel"])},
+    }
+    if attention is not None:
+        att = {k: v for k, v in attention.items() if not k.startswith("_")}
+        att["roofline"] = {"bound": "mfma", "achieved": attention["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
+                           "unit": "TFLOP/s", "frac": attention["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+                           "traffic": traffic_from_profiles(attention["kernel"])}
+        line["attention"] = att
+    if not args.no_cpu_baseline and gemm is not None:
+        log("cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline(gemm, attention)
+    line["extra"] = extra
+    line["gpu_kernel"] = {k: v for k, v in head.items() if not k.startswith("_")}
+    print(json.dumps(line), flush=True)
+    rt.close()
+
+
+if __name__ == "__main__":
+    main()

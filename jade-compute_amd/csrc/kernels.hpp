@@ -1,0 +1,61 @@
+// Host-side launchers for the hand-written gfx950 kernels. Every launcher
+// checks nothing about buffer ownership: the runtime has already validated
+// binding counts, exact lengths and aliasing before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "spec.hpp"
+
+namespace jade {
+namespace hipk {
+
+struct LaunchShape {
+    const char *kernel;
+    uint32_t grid[3];
+    uint32_t block[3];
+    uint32_t lds_bytes;
+};
+
+// C[m,n] = A[m,k] * B[k,n], packed row-major FP32, FP32 MFMA accumulate.
+LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k);
+hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
+                    uint32_t k);
+
+// Flash-style online softmax(Q K^T / sqrt(dim)) V, [heads, seq, dim] contiguous.
+LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
+hipError_t attention_online_f32(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
+                                uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
+
+// Materialised comparator: scaled scores [heads, seq, seq] (-inf above the
+// causal diagonal) and probabilities x V.
+LaunchShape attention_scores_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
+hipError_t attention_scores_f32(hipStream_t stream, const float *q, const float *k, float *scores, uint32_t heads,
+                                uint32_t seq, uint32_t dim, bool causal);
+LaunchShape attention_apply_shape(uint32_t heads, uint32_t seq, uint32_t dim);
+hipError_t attention_apply_f32(hipStream_t stream, const float *p, const float *v, float *out, uint32_t heads,
+                               uint32_t seq, uint32_t dim);
+
+// Row kernels: one row per 64-lane wavefront.
+LaunchShape rms_norm_shape(uint32_t rows, uint32_t cols);
+hipError_t rms_norm_f32(hipStream_t stream, const float *x, const float *weight, float *out, uint32_t rows,
+                        uint32_t cols, float epsilon);
+LaunchShape softmax_shape(uint32_t rows, uint32_t cols);
+hipError_t softmax_f32(hipStream_t stream, const float *x, float *out, uint32_t rows, uint32_t cols);
+
+// Streaming elementwise kernels.
+LaunchShape stream_shape(uint32_t len);
+hipError_t swiglu_f32(hipStream_t stream, const float *gate, const float *up, float *out, uint32_t len);
+hipError_t add_f32(hipStream_t stream, const float *a, const float *b, float *out, uint32_t len);
+hipError_t axpy_f32(hipStream_t stream, float alpha, const float *a, const float *b, float *out, uint32_t len);
+hipError_t copy_f32(hipStream_t stream, const float *in, float *out, uint32_t len);
+
+// Postfix-expression interpreter over <= 8 inputs; `program` is device memory.
+LaunchShape elementwise_shape(uint32_t len);
+hipError_t elementwise_f32(hipStream_t stream, const float *const *inputs, uint32_t input_count, float *out,
+                           uint32_t len, const Instr *program, uint32_t program_len);
+
+}  // namespace hipk
+}  // namespace jade

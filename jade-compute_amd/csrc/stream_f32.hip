@@ -1,0 +1,134 @@
+// Streaming elementwise kernels: Add (ir.rs:486), Axpy (ir.rs:485, fma(alpha,
+// a, b)), SwiGLU (ir.rs:487, g * sigmoid(g) * u with the stable sigmoid
+// e = exp(-|g|), g >= 0 ? 1/(1+e) : e/(1+e)), a plain copy, and the
+// Elementwise expression interpreter (ir.rs:111-137, 484).
+// Each thread owns one 16-byte slot (4 floats); the final partial slot of a
+// length that is not a multiple of 4 falls back to scalar accesses.
+#include "kernels.hpp"
+
+#include <cmath>
+
+namespace jade {
+namespace hipk {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ inline float swiglu(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-fabsf(g) * kLog2e);
+    const float sigmoid = g >= 0.f ? 1.0f / (1.0f + e) : e / (1.0f + e);
+    return (g * sigmoid) * u;
+}
+
+struct AddOp {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct AxpyOp {
+    float alpha;
+    __device__ float operator()(float a, float b) const { return fmaf(alpha, a, b); }
+};
+struct SwiGluOp {
+    __device__ float operator()(float g, float u) const { return swiglu(g, u); }
+};
+
+template <typename F>
+__global__ __launch_bounds__(kThreads) void binary_stream(const float *__restrict__ a, const float *__restrict__ b,
+                                                          float *__restrict__ out, uint32_t len, F f) {
+    const uint32_t slot = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t first = slot * 4u;
+    if (first >= len) return;
+    if (first + 4u <= len) {
+        const f32x4 x = reinterpret_cast<const f32x4 *>(a)[slot];
+        const f32x4 y = reinterpret_cast<const f32x4 *>(b)[slot];
+        reinterpret_cast<f32x4 *>(out)[slot] = f32x4{f(x.x, y.x), f(x.y, y.y), f(x.z, y.z), f(x.w, y.w)};
+    } else {
+        for (uint32_t i = first; i < len; ++i) out[i] = f(a[i], b[i]);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void copy_stream(const float *__restrict__ in, float *__restrict__ out,
+                                                        uint32_t len) {
+    const uint32_t slot = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t first = slot * 4u;
+    if (first >= len) return;
+    if (first + 4u <= len) {
+        reinterpret_cast<f32x4 *>(out)[slot] = reinterpret_cast<const f32x4 *>(in)[slot];
+    } else {
+        for (uint32_t i = first; i < len; ++i) out[i] = in[i];
+    }
+}
+
+struct InputTable {
+    const float *in[kMaxElementwiseInputs];
+};
+
+// One element per thread; the program is wave-uniform, so its words are
+// scalar loads. Constants travel as raw f32 bits.
+__global__ __launch_bounds__(kThreads) void expression_interpreter(InputTable inputs, float *__restrict__ out,
+                                                                   uint32_t len, const Instr *__restrict__ program,
+                                                                   uint32_t count) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= len) return;
+    float stack[kMaxExprStack];
+    int sp = 0;
+    for (uint32_t pc = 0; pc < count; ++pc) {
+        const Instr ins = program[pc];
+        switch (ins.op) {
+            case uint32_t(Opcode::Input): stack[sp++] = inputs.in[ins.arg][i]; break;
+            case uint32_t(Opcode::Constant): stack[sp++] = __uint_as_float(ins.arg); break;
+            case uint32_t(Opcode::Add): --sp; stack[sp - 1] = stack[sp - 1] + stack[sp]; break;
+            case uint32_t(Opcode::Multiply): --sp; stack[sp - 1] = stack[sp - 1] * stack[sp]; break;
+            case uint32_t(Opcode::Maximum): --sp; stack[sp - 1] = fmaxf(stack[sp - 1], stack[sp]); break;
+            case uint32_t(Opcode::Negate): stack[sp - 1] = -stack[sp - 1]; break;
+            default: stack[sp - 1] = expf(stack[sp - 1]); break;
+        }
+    }
+    out[i] = stack[0];
+}
+
+dim3 slots_grid(uint32_t len) { return dim3(((len + 3u) / 4u + kThreads - 1) / kThreads); }
+
+template <typename F>
+hipError_t launch_binary(hipStream_t stream, const float *a, const float *b, float *out, uint32_t len, F f) {
+    hipLaunchKernelGGL((binary_stream<F>), slots_grid(len), dim3(kThreads), 0, stream, a, b, out, len, f);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+LaunchShape stream_shape(uint32_t len) {
+    return {"binary_stream", {slots_grid(len).x, 1, 1}, {kThreads, 1, 1}, 0};
+}
+
+hipError_t swiglu_f32(hipStream_t stream, const float *gate, const float *up, float *out, uint32_t len) {
+    return launch_binary(stream, gate, up, out, len, SwiGluOp{});
+}
+hipError_t add_f32(hipStream_t stream, const float *a, const float *b, float *out, uint32_t len) {
+    return launch_binary(stream, a, b, out, len, AddOp{});
+}
+hipError_t axpy_f32(hipStream_t stream, float alpha, const float *a, const float *b, float *out, uint32_t len) {
+    return launch_binary(stream, a, b, out, len, AxpyOp{alpha});
+}
+hipError_t copy_f32(hipStream_t stream, const float *in, float *out, uint32_t len) {
+    hipLaunchKernelGGL(copy_stream, slots_grid(len), dim3(kThreads), 0, stream, in, out, len);
+    return hipGetLastError();
+}
+
+LaunchShape elementwise_shape(uint32_t len) {
+    return {"expression_interpreter", {(len + kThreads - 1) / kThreads, 1, 1}, {kThreads, 1, 1}, 0};
+}
+
+hipError_t elementwise_f32(hipStream_t stream, const float *const *inputs, uint32_t input_count, float *out,
+                           uint32_t len, const Instr *program, uint32_t program_len) {
+    InputTable table{};
+    for (uint32_t i = 0; i < input_count && i < kMaxElementwiseInputs; ++i) table.in[i] = inputs[i];
+    hipLaunchKernelGGL(expression_interpreter, dim3((len + kThreads - 1) / kThreads), dim3(kThreads), 0, stream,
+                       table, out, len, program, program_len);
+    return hipGetLastError();
+}
+
+}  // namespace hipk
+}  // namespace jade

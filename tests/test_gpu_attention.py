@@ -1,0 +1,118 @@
+"""Online (flash-style) FP32 attention parity against the FP64 materialised
+oracle (src/runtime/metal_lab.rs:33-73).
+
+Cases: the reference's metal-verify attention configs (metal_lab.rs:419-431,
+inputs at :276-286, tolerance 5e-5, or 5e-4 for amplitude > 1, at :333), its
+oracle KAT (:472-484), the materialised scores -> softmax -> apply chain
+(:295-324), config C3 (B1 H8 S1024 D64, N(0,1)) and the LLM config (B4 H32
+S4096 D128 causal) on query-row windows, gated at |a-e| <= 2e-4 + 2e-4|e|.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle_binding as orc
+
+pytestmark = pytest.mark.gpu
+
+NORTH_STAR_TOL = 2e-4
+
+
+def run_online(runtime, h, s, d, causal, q, k, v, repeats=1):
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
+    qg, kg, vg = runtime.resident(q), runtime.resident(k), runtime.resident(v)
+    out = runtime.alloc(h * s * d)
+    runtime.execute([(kernel, [qg, kg, vg, out])], repeats)
+    got = runtime.download(out)
+    assert np.array_equal(runtime.download(qg), q) and np.array_equal(runtime.download(vg), v)
+    for x in (qg, kg, vg, out):
+        x.free()
+    return got
+
+
+def run_materialised(runtime, h, s, d, causal, q, k, v):
+    scores = runtime.compile({"op": "attention_scores", "heads": h, "seq": s, "dim": d, "causal": causal})
+    softmax = runtime.compile({"op": "softmax", "rows": h * s, "cols": s})
+    apply = runtime.compile({"op": "attention_apply", "heads": h, "seq": s, "dim": d})
+    qg, kg, vg = runtime.resident(q), runtime.resident(k), runtime.resident(v)
+    sc, pr, out = runtime.alloc(h * s * s), runtime.alloc(h * s * s), runtime.alloc(h * s * d)
+    runtime.execute([(scores, [qg, kg, sc]), (softmax, [sc, pr]), (apply, [pr, vg, out])], 1)
+    return runtime.download(out)
+
+
+LAB = [(1, 1, 1, False, 1.0, False), (1, 1, 128, True, 1.0, False), (2, 7, 17, False, 1.0, False),
+       (2, 7, 17, True, 1.0, False), (2, 33, 64, False, 1.0, False), (2, 33, 64, True, 1.0, False),
+       (1, 65, 128, True, 1.0, False), (3, 17, 33, False, 1.0, True), (2, 17, 31, True, 1.0, True),
+       (2, 17, 64, False, 20.0, False), (2, 17, 64, True, 20.0, False)]
+
+
+@pytest.mark.parametrize("h,s,d,causal,amp,zeros", LAB)
+def test_lab_attention_configs(runtime, h, s, d, causal, amp, zeros):
+    n = h * s * d
+    q = np.zeros(n, np.float32) if zeros else orc.values(n, 0x1111, amp)
+    k = np.zeros(n, np.float32) if zeros else orc.values(n, 0x2222, amp)
+    v = orc.values(n, 0x3333, 1.0)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    tol = 5e-4 if amp > 1.0 else 5e-5
+    for got in (run_online(runtime, h, s, d, causal, q, k, v, repeats=3),
+                run_materialised(runtime, h, s, d, causal, q, k, v)):
+        check = orc.compare(got, want, tol, tol)
+        assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+def test_oracle_kat_on_device(runtime):
+    q = np.zeros(6, np.float32)
+    v = np.array([1, 2, 3, 4, 8, 9], np.float32)
+    np.testing.assert_allclose(run_online(runtime, 1, 3, 2, False, q, q, v), [4, 5, 4, 5, 4, 5], rtol=1e-6)
+    np.testing.assert_allclose(run_online(runtime, 1, 3, 2, True, q, q, v), [1, 2, 2, 3, 4, 5], rtol=1e-6)
+
+
+@pytest.mark.parametrize("h,s,d", [(3, 129, 96), (1, 300, 40), (2, 257, 128), (4, 130, 3), (1, 1000, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_ragged_tiles_and_padded_head_dims(runtime, h, s, d, causal):
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x1111), orc.normal(n, 0x2222), orc.normal(n, 0x3333)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    got = run_online(runtime, h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_config_c3(runtime, causal):
+    h, s, d = 8, 1024, 64
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x1111), orc.normal(n, 0x2222), orc.normal(n, 0x3333)
+    got = run_online(runtime, h, s, d, causal, q, k, v)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+def test_config_llm_causal_row_windows(runtime):
+    h, s, d = 4 * 32, 4096, 128
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x1111), orc.normal(n, 0x2222), orc.normal(n, 0x3333)
+    got = run_online(runtime, h, s, d, True, q, k, v).reshape(h, s, d)
+    for r0, r1 in ((0, 4), (2046, 2050), (4092, 4096)):
+        want = orc.attention_reference(h, s, d, True, q, k, v, rows=(r0, r1)).reshape(h, r1 - r0, d)
+        check = orc.compare(got[:, r0:r1].reshape(-1), want.reshape(-1), NORTH_STAR_TOL, NORTH_STAR_TOL)
+        assert check.status == 0, (r0, check.first_bad)
+    # Causal row 0 attends to key 0 only.
+    np.testing.assert_array_equal(got[:, 0], v.reshape(h, s, d)[:, 0])
+    assert np.isfinite(got).all()
+
+
+def test_scale_is_one_over_sqrt_dim(runtime):
+    # Two keys whose scores differ by exactly sqrt(d): weights e^1 : 1.
+    h, s, d = 1, 2, 16
+    q = np.zeros((s, d), np.float32)
+    k = np.zeros((s, d), np.float32)
+    q[1, 0] = 1.0
+    k[1, 0] = math.sqrt(d)
+    v = np.zeros((s, d), np.float32)
+    v[0, 0], v[1, 0] = 0.0, 1.0
+    got = run_online(runtime, h, s, d, False, q.reshape(-1), k.reshape(-1), v.reshape(-1)).reshape(s, d)
+    assert got[1, 0] == pytest.approx(math.e / (1.0 + math.e), rel=2e-6)
+    assert got[0, 0] == pytest.approx(0.5, rel=2e-6)

@@ -1,0 +1,135 @@
+"""FP32 MFMA GEMM parity against the FP64 oracle.
+
+Cases: the reference's metal-verify GEMM shapes (src/runtime/metal_lab.rs:
+400-413, inputs at :135-136, tolerance 5e-5 at :173), the `jade-compute
+verify` odd shapes (src/main.rs:250-258, validation::check), its precision
+probes (metal_lab.rs:437-461), and the BASELINE configs: 512^3, the
+1024/2048/4096 squares and the ragged (1000,777,513) and (4096,11008,4096)
+shapes with validation::inputs, gated at |a-e| <= 1e-4 + 1e-4|e|.
+"""
+import numpy as np
+import pytest
+
+import jade_hip
+import oracle_binding as orc
+
+pytestmark = pytest.mark.gpu
+
+NORTH_STAR_TOL = 1e-4
+
+
+def run_gemm(runtime, m, n, k, a, b, spec_op="gemm", repeats=1):
+    spec = {"op": spec_op, "m": m, "n": n, "k": k}
+    if spec_op == "gemm":
+        spec["tiled"] = True
+    kernel = runtime.compile(spec)
+    ag, bg, out = runtime.resident(a), runtime.resident(b), runtime.alloc(m * n)
+    runtime.execute([(kernel, [ag, bg, out])], repeats)
+    got = runtime.download(out)
+    assert np.array_equal(runtime.download(ag), a) and np.array_equal(runtime.download(bg), b), "input modified"
+    for x in (ag, bg, out):
+        x.free()
+    return got
+
+
+LAB_SHAPES = [(1, 1, 1), (7, 9, 13), (8, 8, 8), (31, 47, 19), (32, 32, 33), (33, 31, 65), (65, 67, 63),
+              (1, 129, 33), (64, 64, 64), (127, 65, 129), (256, 256, 65), (257, 263, 67)]
+
+
+@pytest.mark.parametrize("m,n,k", LAB_SHAPES)
+@pytest.mark.parametrize("op", ["gemm", "gemm_simd"])
+def test_lab_gemm_shapes(runtime, m, n, k, op):
+    a = orc.values(m * k, 0x1234, 1.0)
+    b = orc.values(k * n, 0xABCD, np.float32(1.0) / np.sqrt(np.float32(k)))
+    want = orc.gemm_reference(m, n, k, a, b)
+    got = run_gemm(runtime, m, n, k, a, b, op, repeats=3)
+    check = orc.compare(got, want, 5e-5, 5e-5)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (1, 17, 33), (17, 1, 35), (31, 47, 19), (64, 64, 64), (65, 33, 17),
+                                   (3, 5, 257)])
+def test_jade_compute_verify_shapes(runtime, m, n, k):
+    a, b = orc.inputs(m, n, k)
+    got = run_gemm(runtime, m, n, k, a, b)
+    result = orc.check_gemm(m, n, k, a, b, got, 1 << 62)
+    assert result.status == 0 and result.checked_elements == m * n
+    assert orc.compare(got, orc.gemm_reference(m, n, k, a, b), NORTH_STAR_TOL, NORTH_STAR_TOL).status == 0
+
+
+@pytest.mark.parametrize("a,b", [(1.0001, 1.0003), (70000.25, 1.0000312)])
+def test_fp32_precision_probes(runtime, a, b):
+    av, bv = np.array([a], np.float32), np.array([b], np.float32)
+    for op in ("gemm_simd", "gemm"):
+        got = run_gemm(runtime, 1, 1, 1, av, bv, op)
+        assert orc.compare(got, [float(av[0]) * float(bv[0])], 1e-5, 1e-6).status == 0
+
+
+def gate(got, m, n, k, a, b, rows=None):
+    want = orc.gemm_reference(m, n, k, a, b, rows=rows)
+    part = got if rows is None else got[rows[0] * n:rows[1] * n]
+    check = orc.compare(part, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, part[check.first_bad], want[check.first_bad])
+    return check
+
+
+@pytest.mark.parametrize("m,n,k", [(512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513)])
+def test_config_gemm_full_oracle(runtime, m, n, k):
+    a, b = orc.inputs(m, n, k)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b)
+    assert orc.check_gemm(m, n, k, a, b, got, 4096).status == 0
+
+
+def test_config_gemm_4096_cubed(runtime):
+    m = n = k = 4096
+    a, b = orc.inputs(m, n, k)
+    got = run_gemm(runtime, m, n, k, a, b)
+    for rows in ((0, 96), (2000, 2096), (4000, 4096)):
+        gate(got, m, n, k, a, b, rows)
+    assert orc.check_gemm(m, n, k, a, b, got, 8192).status == 0
+
+
+def test_config_gemm_llm_shape(runtime):
+    m, n, k = 4096, 11008, 4096
+    a, b = orc.inputs(m, n, k)
+    got = run_gemm(runtime, m, n, k, a, b)
+    for rows in ((0, 32), (2040, 2072), (4064, 4096)):
+        gate(got, m, n, k, a, b, rows)
+    assert orc.check_gemm(m, n, k, a, b, got, 8192).status == 0
+
+
+@pytest.mark.parametrize("m,n,k", [(129, 130, 131), (255, 257, 4), (3, 4100, 7), (4100, 3, 9), (128, 128, 1),
+                                   (200, 8, 1000)])
+def test_edge_masking_shapes(runtime, m, n, k):
+    a = orc.values(m * k, 0x55, 1.0)
+    b = orc.values(k * n, 0x66, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b)
+
+
+def test_gemm_plan_abi_bench_flow():
+    # src/main.rs:281-310 driving src/corex.rs through native/jade_corex.h.
+    m = n = k = 512
+    a, b = orc.inputs(m, n, k)
+    plan = jade_hip.GemmPlan(m, n, k)
+    try:
+        assert "gfx950" in plan.device_info()
+        with pytest.raises(jade_hip.JadeError):
+            plan.run(1)  # upload first
+        with pytest.raises(jade_hip.JadeError):
+            plan.download()
+        with pytest.raises(jade_hip.JadeError):
+            plan.upload(a[:-1], b)
+        plan.upload(a, b)
+        ms = plan.run(1)
+        assert ms > 0
+        out = plan.download()
+        assert orc.check_gemm(m, n, k, a, b, out, 4096).status == 0
+        assert orc.compare(out, orc.gemm_reference(m, n, k, a, b), NORTH_STAR_TOL, NORTH_STAR_TOL).status == 0
+        assert plan.run(3) > 0
+        with pytest.raises(jade_hip.JadeError):
+            plan.run(0)  # rejected before touching state (native/jade_corex.cpp:216-217)
+        np.testing.assert_array_equal(plan.download(), out)
+    finally:
+        plan.close()

@@ -1,0 +1,156 @@
+"""KernelSpec parsing and validation (the reference's IR, src/runtime/ir.rs),
+checked on the CPU through the context-free C entry points."""
+import json
+import os
+
+import pytest
+
+import jade_hip
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "spec_fixtures.json")
+FIXTURES = json.load(open(GOLDEN))
+
+
+def describe(spec):
+    return jade_hip.spec_describe(spec)
+
+
+def rejected(spec):
+    with pytest.raises(jade_hip.JadeError) as info:
+        describe(spec)
+    assert info.value.code == 1
+    return info.value.message
+
+
+@pytest.mark.parametrize("case", FIXTURES["cases"], ids=lambda c: c["case"])
+def test_verify_suite_specs_parse_with_reference_bindings(case):
+    # Spec files and binding manifest written by the reference's emit-suite.
+    d = describe(case["spec_file_text"])
+    assert d["bindings"] == case["bindings"]
+    assert d["reference_valid"] and d["hip_supported"]
+    assert json.loads(json.dumps(d["spec"])) == d["spec"]
+    again = describe(json.dumps(d["spec"]))  # canonical form round-trips
+    assert again == d
+    # Field values survive the round trip.
+    for key, value in case["spec"].items():
+        if key not in ("expression",):
+            assert d["spec"][key] == pytest.approx(value) if isinstance(value, float) else d["spec"][key] == value
+
+
+def test_example_specs():
+    by_name = {e["file"]: e["text"] for e in FIXTURES["examples"]}
+    relu = describe(by_name["fused_axpy_relu.json"])
+    assert relu["name"] == "elementwise" and len(relu["bindings"]) == 3
+    att = describe(by_name["attention_online.json"])
+    assert att["name"] == "attention_online" and att["reference_valid"]
+    assert [b["elements"] for b in att["bindings"]] == [4 * 256 * 64] * 4
+    simd = describe(by_name["gemm_simd.json"])
+    assert simd["name"] == "gemm_simdgroup_fp32" and simd["hip_supported"]
+    mps = describe(by_name["gemm_mps.json"])
+    assert not mps["hip_supported"] and mps["launch"] is None and "MPS" in mps["hip_error"]
+
+
+@pytest.mark.parametrize("op", ["gemm_simd", "attention_online", "attention_scores", "attention_apply"])
+def test_specific_ops_validate_bindings_and_reject_write_alias(op):
+    # src/runtime/ir.rs:582-625.
+    spec = {"gemm_simd": {"op": "gemm_simd", "m": 33, "n": 17, "k": 65},
+            "attention_online": {"op": "attention_online", "heads": 2, "seq": 33, "dim": 17, "causal": True},
+            "attention_scores": {"op": "attention_scores", "heads": 2, "seq": 33, "dim": 17, "causal": True},
+            "attention_apply": {"op": "attention_apply", "heads": 2, "seq": 33, "dim": 17}}[op]
+    lengths = [b["elements"] for b in describe(spec)["bindings"]]
+    ids = list(range(len(lengths)))
+    jade_hip.spec_validate_bindings(spec, lengths, ids)
+    ids[-1] = 0
+    with pytest.raises(jade_hip.JadeError):
+        jade_hip.spec_validate_bindings(spec, lengths, ids)
+
+
+U32_MAX = 4294967295
+
+
+@pytest.mark.parametrize("heads,seq,dim", [(0, 1, 1), (33, 1, 1), (1, 0, 1), (1, 2049, 1), (1, 1, 0), (1, 1, 129),
+                                           (U32_MAX, U32_MAX, U32_MAX)])
+def test_attention_shape_limits(heads, seq, dim):
+    # src/runtime/ir.rs:626-643 rejects all of these; the HIP rules lift only
+    # the Metal-era heads <= 32 and seq <= 2048 caps.
+    spec = {"op": "attention_online", "heads": heads, "seq": seq, "dim": dim, "causal": False}
+    if (heads, seq, dim) in ((33, 1, 1), (1, 2049, 1)):
+        d = describe(spec)
+        assert not d["reference_valid"] and d["hip_supported"]
+    else:
+        rejected(spec)
+
+
+def test_llm_attention_config_is_valid_on_hip_only():
+    d = describe({"op": "attention_online", "heads": 128, "seq": 4096, "dim": 128, "causal": True})
+    assert not d["reference_valid"] and "heads" in d["reference_error"]
+    assert d["bindings"][0]["elements"] == 128 * 4096 * 128
+    # The materialised score tensor would need heads*seq*seq > INT_MAX elements.
+    rejected({"op": "attention_scores", "heads": 128, "seq": 4096, "dim": 128, "causal": True})
+
+
+def test_gemm_and_invalid_semantics():
+    # src/runtime/ir.rs:644-650, 676-702.
+    rejected({"op": "gemm_simd", "m": U32_MAX, "n": U32_MAX, "k": U32_MAX})
+    rejected({"op": "gemm", "m": U32_MAX, "n": 2, "k": 1, "tiled": True})
+    assert "epsilon" in rejected({"op": "rms_norm", "rows": 1, "cols": 17, "epsilon": 0.0})
+    assert "alpha" in rejected({"op": "axpy", "len": 1, "alpha": 1e39})  # overflows f32 to infinity
+    spec = {"op": "add", "len": 17}
+    with pytest.raises(jade_hip.JadeError):
+        jade_hip.spec_validate_bindings(spec, [17, 17, 17], [1, 2, 1])
+    with pytest.raises(jade_hip.JadeError):
+        jade_hip.spec_validate_bindings(spec, [17, 16, 17], [1, 2, 3])
+    jade_hip.spec_validate_bindings(spec, [17, 17, 17], [1, 1, 3])  # read/read aliasing is fine
+    with pytest.raises(jade_hip.JadeError):
+        jade_hip.spec_validate_bindings(spec, [17, 17], [1, 2])
+
+
+def _negates(count):
+    e = {"kind": "input", "binding": 0}
+    for _ in range(count):
+        e = {"kind": "negate", "value": e}
+    return e
+
+
+def test_expression_limits():
+    # src/runtime/ir.rs:86-110, 653-674.
+    rejected({"op": "elementwise", "len": 7, "inputs": 1, "expression": {"kind": "input", "binding": 1}})
+    describe({"op": "elementwise", "len": 7, "inputs": 1, "expression": _negates(32)})
+    assert "complexity" in rejected({"op": "elementwise", "len": 7, "inputs": 1, "expression": _negates(33)})
+    rejected({"op": "elementwise", "len": 7, "inputs": 9, "expression": {"kind": "input", "binding": 0}})
+    rejected({"op": "elementwise", "len": 7, "inputs": 0, "expression": {"kind": "input", "binding": 0}})
+
+    def tree(depth):  # complete binary tree: 2^(depth+1)-1 nodes
+        if depth == 0:
+            return {"kind": "constant", "value": 1.0}
+        return {"kind": "add", "left": tree(depth - 1), "right": tree(depth - 1)}
+
+    describe({"op": "elementwise", "len": 3, "inputs": 1, "expression": tree(7)})  # 255 nodes
+    big = {"kind": "add", "left": tree(7), "right": tree(7)}  # 511 nodes
+    describe({"op": "elementwise", "len": 3, "inputs": 1, "expression": big})
+    bigger = {"kind": "add", "left": big, "right": {"kind": "constant", "value": 2.0}}  # 513 nodes
+    rejected({"op": "elementwise", "len": 3, "inputs": 1, "expression": bigger})
+
+
+def test_serde_shape_rules():
+    assert "missing field" in rejected({"op": "gemm", "m": 1, "n": 1, "k": 1})
+    assert "unknown variant" in rejected({"op": "conv2d", "len": 1})
+    rejected({"op": "add", "len": -1})
+    rejected({"op": "add", "len": 1.5})
+    rejected({"op": "add", "len": U32_MAX + 1})
+    rejected({"op": "gemm", "m": 1, "n": 1, "k": 1, "tiled": 1})
+    rejected('{"op": "add", "len": 3')
+    rejected('{"op": "add", "len": 3, "len": 4}')
+    d = describe({"op": "add", "len": 3, "comment": "unknown members are ignored"})
+    assert d["spec"] == {"op": "add", "len": 3}
+    rejected({"op": "add", "len": 0})
+    rejected("x" * 70000)  # over the 64 KiB spec cap
+
+
+def test_constant_bits_round_trip():
+    for value in (2.5, 1e-5, -0.375, 3.4028234663852886e38, 1.17549435e-38):
+        spec = {"op": "elementwise", "len": 1, "inputs": 1,
+                "expression": {"kind": "constant", "value": value}}
+        d = describe(spec)
+        import numpy as np
+        assert np.float32(d["spec"]["expression"]["value"]) == np.float32(value)
