@@ -90,15 +90,16 @@ def test_config_c3(runtime, causal):
     assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
 
 
-def test_config_llm_causal_row_windows(runtime):
+def test_config_llm_causal_full_output(runtime):
     h, s, d = 4 * 32, 4096, 128
     n = h * s * d
     q, k, v = orc.normal(n, 0x1111), orc.normal(n, 0x2222), orc.normal(n, 0x3333)
     got = run_online(runtime, h, s, d, True, q, k, v).reshape(h, s, d)
-    for r0, r1 in ((0, 4), (2046, 2050), (4092, 4096)):
+    for r0, r1 in ((0, 1024), (1024, 2048), (2048, 3072), (3072, 4096)):
         want = orc.attention_reference(h, s, d, True, q, k, v, rows=(r0, r1)).reshape(h, r1 - r0, d)
         check = orc.compare(got[:, r0:r1].reshape(-1), want.reshape(-1), NORTH_STAR_TOL, NORTH_STAR_TOL)
         assert check.status == 0, (r0, check.first_bad)
+        print(f"rows {r0}..{r1} max_abs {check.max_abs_error:.3e} max_rel {check.max_relative_error:.3e}")
     # Causal row 0 attends to key 0 only.
     np.testing.assert_array_equal(got[:, 0], v.reshape(h, s, d)[:, 0])
     assert np.isfinite(got).all()

@@ -85,8 +85,8 @@ def test_config_gemm_4096_cubed(runtime):
     m = n = k = 4096
     a, b = orc.inputs(m, n, k)
     got = run_gemm(runtime, m, n, k, a, b)
-    for rows in ((0, 96), (2000, 2096), (4000, 4096)):
-        gate(got, m, n, k, a, b, rows)
+    check = gate(got, m, n, k, a, b)  # every element
+    print(f"4096^3 max_abs {check.max_abs_error:.3e} max_rel {check.max_relative_error:.3e}")
     assert orc.check_gemm(m, n, k, a, b, got, 8192).status == 0
 
 
@@ -94,7 +94,7 @@ def test_config_gemm_llm_shape(runtime):
     m, n, k = 4096, 11008, 4096
     a, b = orc.inputs(m, n, k)
     got = run_gemm(runtime, m, n, k, a, b)
-    for rows in ((0, 32), (2040, 2072), (4064, 4096)):
+    for rows in ((0, 1024), (1024, 2048), (2048, 3072), (3072, 4096)):
         gate(got, m, n, k, a, b, rows)
     assert orc.check_gemm(m, n, k, a, b, got, 8192).status == 0
 
