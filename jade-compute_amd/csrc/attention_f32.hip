@@ -3,16 +3,22 @@
 // O = softmax(Q K^T / sqrt(dim)) V, scale 1/sqrt(float(dim)) in FP32, causal rows
 // keep keys <= query (diagonal included), online max/normaliser recurrence.
 //
-// Flash-style kernel for CDNA4. One wave owns 32 queries; a 256-thread block
-// owns 128 queries of one head and streams K/V through LDS in 32-key tiles.
-// Both products run on v_mfma_f32_32x32x2_f32 in transposed form:
+// Flash-style kernel for CDNA4. One wave owns 32 queries; a block of NW waves
+// owns 32*NW queries of one head and streams K/V through LDS in 64-key tiles,
+// double-buffered with a register prefetch of the next tile (one barrier per
+// tile). Both products run on v_mfma_f32_32x32x2_f32 in transposed form:
 //   S^T[key, q] = sum_d K[key, d] Q[q, d]        (A = K from LDS, B = Q^T in registers)
 //   O^T[d, q]  += sum_key V^T[d, key] P^T[key, q] (A = V^T from LDS, B = P^T in registers)
 // The S^T accumulator leaves lane l holding query l%32 for 16 keys, and exactly
 // those 16 values are the B operand the P.V product needs from lane l, so the
 // probabilities never leave registers. Row max and row sum over a tile are a
-// 16-value local reduction plus one exchange with lane l^32. Scores are kept in
-// log2 units (Q pre-scaled by scale*log2(e)) so each probability is one v_exp_f32.
+// local reduction plus one exchange with lane l^32. Scores are kept in log2
+// units (Q pre-scaled by scale*log2(e)) so each probability is one v_exp_f32.
+//
+// Scheduling: grid = (heads, query blocks) with the query-block index reversed,
+// so the longest causal rows of every head dispatch first, and all blocks of a
+// head share one XCD (workgroups go round-robin over 8 XCDs by linear id). A
+// wave skips 32-key sub-tiles that lie wholly above its causal diagonal.
 #include "kernels.hpp"
 
 #include <cmath>
@@ -24,27 +30,83 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kThreads = 256;
-constexpr int kBQ = 128;   // queries per block (4 waves x 32)
-constexpr int kBKV = 32;   // keys per LDS tile
+constexpr int kBKV = 64;  // keys per LDS tile (two 32-key sub-tiles)
 constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
 
-template <int DP, bool CAUSAL, bool VEC>
-__global__ __launch_bounds__(kThreads) void attention_online_mfma(const float *__restrict__ Q,
-                                                                  const float *__restrict__ K,
-                                                                  const float *__restrict__ V,
-                                                                  float *__restrict__ O, int seq, int dim,
-                                                                  float qscale, int q_blocks) {
-    constexpr int LD = DP + 4;  // LDS row stride (floats); keeps float4 alignment
+template <int DP, int NW>
+struct AttnShape {
+    static constexpr int kThreads = NW * 64;
+    static constexpr int kBQ = NW * 32;
+    static constexpr int kLD = DP + 4;             // LDS row stride (floats), float4-aligned
+    static constexpr int kTile = kBKV * kLD;       // floats in one K (or V) tile
+    static constexpr int kLoads = kBKV * DP / 4 / kThreads;  // float4 per thread per tensor
+    static constexpr uint32_t kLdsBytes = 2u * 2u * kTile * sizeof(float);
+    static_assert(kLoads >= 1 && kBKV * DP / 4 % kThreads == 0, "tile must split evenly over the block");
+};
+
+// Global -> registers for one K/V tile (rows [kt, kt+64), zero past seq/dim).
+template <int DP, int NW, bool VEC>
+__device__ inline void load_kv(const float *__restrict__ K, const float *__restrict__ V, size_t base, int kt,
+                               int seq, int dim, f32x4 (&pk)[AttnShape<DP, NW>::kLoads],
+                               f32x4 (&pv)[AttnShape<DP, NW>::kLoads]) {
+    using S = AttnShape<DP, NW>;
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+        const int idx = threadIdx.x + i * S::kThreads;
+        const int r = idx / (DP / 4), c4 = (idx % (DP / 4)) * 4;
+        const int key = kt + r;
+        f32x4 kv = {0.f, 0.f, 0.f, 0.f}, vv = {0.f, 0.f, 0.f, 0.f};
+        if (key < seq) {
+            const size_t off = base + size_t(key) * dim + c4;
+            if (VEC) {
+                if (c4 < dim) {
+                    kv = *reinterpret_cast<const f32x4 *>(K + off);
+                    vv = *reinterpret_cast<const f32x4 *>(V + off);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (c4 + e < dim) {
+                        kv[e] = K[off + e];
+                        vv[e] = V[off + e];
+                    }
+                }
+            }
+        }
+        pk[i] = kv;
+        pv[i] = vv;
+    }
+}
+
+template <int DP, int NW>
+__device__ inline void store_kv(float *stage, const f32x4 (&pk)[AttnShape<DP, NW>::kLoads],
+                                const f32x4 (&pv)[AttnShape<DP, NW>::kLoads]) {
+    using S = AttnShape<DP, NW>;
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+        const int idx = threadIdx.x + i * S::kThreads;
+        const int r = idx / (DP / 4), c4 = (idx % (DP / 4)) * 4;
+        *reinterpret_cast<f32x4 *>(stage + r * S::kLD + c4) = pk[i];
+        *reinterpret_cast<f32x4 *>(stage + S::kTile + r * S::kLD + c4) = pv[i];
+    }
+}
+
+template <int DP, int NW, bool CAUSAL, bool VEC>
+__global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__restrict__ Q,
+                                                                 const float *__restrict__ K,
+                                                                 const float *__restrict__ V,
+                                                                 float *__restrict__ O, int seq, int dim,
+                                                                 float qscale) {
+    using S = AttnShape<DP, NW>;
     constexpr int HALF = DP / 2;
-    __shared__ float ks[kBKV * LD];
-    __shared__ float vs[kBKV * LD];
+    constexpr int LD = S::kLD;
+    __shared__ float lds[2 * 2 * S::kTile];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = lane >> 5, c = lane & 31;
-    const int qb = q_blocks - 1 - int(blockIdx.x);  // longest causal rows first
-    const size_t base = size_t(blockIdx.y) * size_t(seq) * size_t(dim);
-    const int q0 = qb * kBQ + wave * 32;
+    const int qb = int(gridDim.y) - 1 - int(blockIdx.y);  // longest causal rows first
+    const size_t base = size_t(blockIdx.x) * size_t(seq) * size_t(dim);
+    const int q0 = qb * S::kBQ + wave * 32;
     const int qi = q0 + c;
 
     // Q^T operand: lane half h holds dims [h*HALF, h*HALF + HALF) of query qi.
@@ -62,82 +124,87 @@ __global__ __launch_bounds__(kThreads) void attention_online_mfma(const float *_
         for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
     float row_max = -INFINITY, row_sum = 0.f;
 
-    const int kv_end = CAUSAL ? min(seq, qb * kBQ + kBQ) : seq;
-    for (int kt = 0; kt < kv_end; kt += kBKV) {
-        __syncthreads();
-        // Stage K and V rows [kt, kt+32) into LDS, zero-padded past seq and dim.
-        for (int idx = threadIdx.x; idx < kBKV * DP / 4; idx += kThreads) {
-            const int r = idx / (DP / 4), c4 = (idx % (DP / 4)) * 4;
-            const int key = kt + r;
-            f32x4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
-            if (key < seq) {
-                const size_t off = base + size_t(key) * dim + c4;
-                if (VEC) {
-                    if (c4 < dim) {
-                        kv4 = *reinterpret_cast<const f32x4 *>(K + off);
-                        vv4 = *reinterpret_cast<const f32x4 *>(V + off);
-                    }
-                } else {
+    const int kv_end = CAUSAL ? min(seq, qb * S::kBQ + S::kBQ) : seq;
+    const int tiles = (kv_end + kBKV - 1) / kBKV;
+    f32x4 pk[S::kLoads], pv[S::kLoads];
+    load_kv<DP, NW, VEC>(K, V, base, 0, seq, dim, pk, pv);
+    store_kv<DP, NW>(lds, pk, pv);
+    __syncthreads();
+
+    for (int t = 0; t < tiles; ++t) {
+        const int kt = t * kBKV;
+        const bool more = t + 1 < tiles;
+        if (more) load_kv<DP, NW, VEC>(K, V, base, kt + kBKV, seq, dim, pk, pv);
+        const float *ks = lds + (t & 1) * 2 * S::kTile;
+        const float *vs = ks + S::kTile;
+        // Sub-tiles of this tile the wave needs: none above its causal diagonal
+        // and none wholly past seq. Wave-uniform.
+        int subs = (kt + 32 < seq) ? 2 : 1;
+        if (CAUSAL) subs = kt > q0 + 31 ? 0 : (kt + 32 > q0 + 31 ? 1 : subs);
+        if (subs > 0) {
+            f32x16 st[2];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (c4 + e < dim) {
-                            kv4[e] = K[off + e];
-                            vv4[e] = V[off + e];
-                        }
+            for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) st[sb][v] = sb < subs ? 0.f : -INFINITY;
+                if (sb < subs) {
+                    const float *krow = ks + (sb * 32 + c) * LD + h * HALF;
+#pragma unroll
+                    for (int s4 = 0; s4 < HALF / 4; ++s4) {
+                        const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * s4);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            st[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qreg[4 * s4 + e], st[sb], 0, 0, 0);
                     }
                 }
             }
-            *reinterpret_cast<f32x4 *>(ks + r * LD + c4) = kv4;
-            *reinterpret_cast<f32x4 *>(vs + r * LD + c4) = vv4;
+            // Mask, then the online max / normaliser update (log2 domain).
+            float tile_max = -INFINITY;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int key = kt + sb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    const bool live = key < seq && (!CAUSAL || key <= qi);
+                    st[sb][v] = live ? st[sb][v] : -INFINITY;
+                    tile_max = fmaxf(tile_max, st[sb][v]);
+                }
+            }
+            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            const float next_max = fmaxf(row_max, tile_max);
+            const float old_weight = __builtin_amdgcn_exp2f(row_max - next_max);
+            float tile_sum = 0.f;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    st[sb][v] = __builtin_amdgcn_exp2f(st[sb][v] - next_max);
+                    tile_sum += st[sb][v];
+                }
+            }
+            tile_sum += __shfl_xor(tile_sum, 32);
+            row_sum = row_sum * old_weight + tile_sum;
+            row_max = next_max;
+#pragma unroll
+            for (int b = 0; b < DP / 32; ++b) acc[b] *= old_weight;
+
+            // O^T += V^T P^T over the live sub-tiles.
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                if (sb < subs) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int key = sb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                        const float *vrow = vs + key * LD + c;
+#pragma unroll
+                        for (int b = 0; b < DP / 32; ++b)
+                            acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[sb][v], acc[b], 0, 0, 0);
+                    }
+                }
+            }
         }
+        if (more) store_kv<DP, NW>(lds + ((t + 1) & 1) * 2 * S::kTile, pk, pv);
         __syncthreads();
-        if (CAUSAL && kt > q0 + 31) continue;  // every query of this wave precedes the tile
-
-        // S^T tile: 32 keys x 32 queries.
-        f32x16 st;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) st[v] = 0.f;
-        const float *krow = ks + c * LD + h * HALF;
-#pragma unroll
-        for (int s4 = 0; s4 < HALF / 4; ++s4) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * s4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) st = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qreg[4 * s4 + e], st, 0, 0, 0);
-        }
-
-        // Mask, then the online max / normaliser update (log2 domain).
-        float tile_max = -INFINITY;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = kt + 8 * (v >> 2) + 4 * h + (v & 3);
-            const bool live = key < seq && (!CAUSAL || key <= qi);
-            st[v] = live ? st[v] : -INFINITY;
-            tile_max = fmaxf(tile_max, st[v]);
-        }
-        tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-        const float next_max = fmaxf(row_max, tile_max);
-        const float old_weight = __builtin_amdgcn_exp2f(row_max - next_max);
-        float tile_sum = 0.f;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            st[v] = __builtin_amdgcn_exp2f(st[v] - next_max);
-            tile_sum += st[v];
-        }
-        tile_sum += __shfl_xor(tile_sum, 32);
-        row_sum = row_sum * old_weight + tile_sum;
-        row_max = next_max;
-#pragma unroll
-        for (int b = 0; b < DP / 32; ++b) acc[b] *= old_weight;
-
-        // O^T += V^T P^T over the tile's 32 keys.
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int key = 8 * (v >> 2) + 4 * h + (v & 3);
-            const float *vrow = vs + key * LD + c;
-#pragma unroll
-            for (int b = 0; b < DP / 32; ++b)
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[v], acc[b], 0, 0, 0);
-        }
     }
 
     if (qi < seq) {
@@ -198,31 +265,56 @@ __global__ __launch_bounds__(256) void attention_apply_kernel(const float *__res
     O[(head * seq + query) * size_t(dim) + channel] = sum;
 }
 
-template <int DP, bool CAUSAL>
+template <int DP, int NW, bool CAUSAL>
 hipError_t launch_online(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                          uint32_t heads, uint32_t seq, uint32_t dim, bool vec) {
-    const int q_blocks = int((seq + kBQ - 1) / kBQ);
+    using S = AttnShape<DP, NW>;
+    const unsigned q_blocks = (seq + S::kBQ - 1) / S::kBQ;
     const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
-    const dim3 grid(unsigned(q_blocks), heads), block(kThreads);
+    const dim3 grid(heads, q_blocks), block(S::kThreads);
     if (vec)
-        hipLaunchKernelGGL((attention_online_mfma<DP, CAUSAL, true>), grid, block, 0, stream, q, k, v, out, int(seq),
-                           int(dim), qscale, q_blocks);
+        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, true>), grid, block, 0, stream, q, k, v, out,
+                           int(seq), int(dim), qscale);
     else
-        hipLaunchKernelGGL((attention_online_mfma<DP, CAUSAL, false>), grid, block, 0, stream, q, k, v, out,
-                           int(seq), int(dim), qscale, q_blocks);
+        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, false>), grid, block, 0, stream, q, k, v, out,
+                           int(seq), int(dim), qscale);
     return hipGetLastError();
 }
 
 int padded_dim(uint32_t dim) { return dim <= 32 ? 32 : dim <= 64 ? 64 : 128; }
 
+// Eight waves per block when that still gives at least two blocks per CU;
+// four waves (128 queries) for small problems so more CUs get work.
+int waves_for(uint32_t heads, uint32_t seq) {
+    const uint64_t blocks8 = uint64_t(heads) * ((seq + 255) / 256);
+    return blocks8 >= 512 ? 8 : 4;
+}
+
+template <int DP>
+hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
+                        uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
+    if (waves_for(heads, seq) == 8)
+        return causal ? launch_online<DP, 8, true>(stream, q, k, v, out, heads, seq, dim, vec)
+                      : launch_online<DP, 8, false>(stream, q, k, v, out, heads, seq, dim, vec);
+    return causal ? launch_online<DP, 4, true>(stream, q, k, v, out, heads, seq, dim, vec)
+                  : launch_online<DP, 4, false>(stream, q, k, v, out, heads, seq, dim, vec);
+}
+
+template <int DP>
+uint32_t lds_bytes(int nw) {
+    return nw == 8 ? AttnShape<DP, 8>::kLdsBytes : AttnShape<DP, 4>::kLdsBytes;
+}
+
 }  // namespace
 
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool) {
     const int dp = padded_dim(dim);
-    const uint32_t lds = 2u * kBKV * (dp + 4) * sizeof(float);
+    const int nw = waves_for(heads, seq);
+    const uint32_t bq = 32u * nw;
+    const uint32_t lds = dp == 32 ? lds_bytes<32>(nw) : dp == 64 ? lds_bytes<64>(nw) : lds_bytes<128>(nw);
     return {dp == 32 ? "attention_online_mfma_d32" : dp == 64 ? "attention_online_mfma_d64" : "attention_online_mfma_d128",
-            {(seq + kBQ - 1) / kBQ, heads, 1},
-            {kThreads, 1, 1},
+            {heads, (seq + bq - 1) / bq, 1},
+            {uint32_t(nw) * 64u, 1, 1},
             lds};
 }
 
@@ -234,15 +326,9 @@ hipError_t attention_online_f32(hipStream_t stream, const float *q, const float 
          15u) == 0;
     const bool vec = aligned && dim % 4 == 0;
     switch (padded_dim(dim)) {
-        case 32:
-            return causal ? launch_online<32, true>(stream, q, k, v, out, heads, seq, dim, vec)
-                          : launch_online<32, false>(stream, q, k, v, out, heads, seq, dim, vec);
-        case 64:
-            return causal ? launch_online<64, true>(stream, q, k, v, out, heads, seq, dim, vec)
-                          : launch_online<64, false>(stream, q, k, v, out, heads, seq, dim, vec);
-        default:
-            return causal ? launch_online<128, true>(stream, q, k, v, out, heads, seq, dim, vec)
-                          : launch_online<128, false>(stream, q, k, v, out, heads, seq, dim, vec);
+        case 32: return dispatch_dim<32>(stream, q, k, v, out, heads, seq, dim, causal, vec);
+        case 64: return dispatch_dim<64>(stream, q, k, v, out, heads, seq, dim, causal, vec);
+        default: return dispatch_dim<128>(stream, q, k, v, out, heads, seq, dim, causal, vec);
     }
 }
 
