@@ -53,29 +53,44 @@ def timed(rt, jobs, steps, warmup):
     return ex.gpu_ms / steps, wall_ms / steps
 
 
-def traffic_from_profiles(kernel_name):
-    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+def traffic_from_profiles(symbol_prefix, launch):
+    """HBM bytes per launch of this kernel at this grid, from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/traffic.json), or None."""
     path = os.path.join(PROFILE_DIR, "traffic.json")
     if not os.path.exists(path):
         return None
+    items = launch["grid"][0] * launch["grid"][1] * launch["grid"][2] * launch["block"][0]
     try:
         table = json.load(open(path))
-        return table.get(kernel_name, {}).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
+    for key, entry in table.items():
+        name, _, grid = key.rpartition("@")
+        if name.startswith(symbol_prefix) and grid == str(items):
+            return entry.get("bytes_per_launch")
+    return None
 
 
 def bench_gemm(rt, m, n, k, steps, warmup, keep=False):
     a = jade_hip.fill_values(m * k, 0x12345678, 1.0)
     b = jade_hip.fill_values(k * n, 0x9ABCDEF1, 1.0)
     kernel = rt.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
-    ag, bg, cg = rt.resident(a), rt.resident(b), rt.alloc(m * n)
+    ag, bg, cg = rt.alloc(m * k), rt.alloc(k * n), rt.alloc(m * n)
+    started = time.perf_counter()
+    rt.upload(ag, a)
+    rt.upload(bg, b)
+    upload_ms = (time.perf_counter() - started) * 1000.0
     ms, wall = timed(rt, [(kernel, [ag, bg, cg])], steps, warmup)
+    started = time.perf_counter()
+    c = rt.download(cg)
+    download_ms = (time.perf_counter() - started) * 1000.0
     flops = 2.0 * m * n * k
     out = {"m": m, "n": n, "k": k, "ms_per_step": ms, "wall_ms_per_step": wall,
-           "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"]}
+           "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"], "launch": kernel.launch,
+           "upload_ms": upload_ms, "download_ms": download_ms,
+           "pcie_inclusive_tflops": flops / ((ms + upload_ms + download_ms) * 1e-3) / 1e12}
     if keep:
-        out["_data"] = (a, b, rt.download(cg))
+        out["_data"] = (a, b, c)
     for x in (ag, bg, cg):
         x.free()
     return out
@@ -92,7 +107,8 @@ def bench_attention(rt, heads, seq, dim, causal, steps, warmup, keep=False):
     keys = seq * (seq + 1) // 2 if causal else seq * seq
     flops = 4.0 * heads * dim * keys
     out = {"heads": heads, "seq": seq, "dim": dim, "causal": causal, "flop": flops, "ms_per_step": ms,
-           "wall_ms_per_step": wall, "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"]}
+           "wall_ms_per_step": wall, "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"],
+           "launch": kernel.launch}
     if keep:
         out["_data"] = (q, k, v, rt.download(bufs[3]))
     for x in bufs:
@@ -157,6 +173,92 @@ def bench_mlp(rt, batch, width, hidden, steps, warmup):
             "per_op": per}
 
 
+COPY_ELEMENTS = 1 << 26  # 256 MiB read + 256 MiB written per launch
+
+
+def bench_copy(rt, steps, warmup):
+    """A plain copy of known size: the calibration point for the HBM counters."""
+    n = COPY_ELEMENTS
+    spec = {"op": "elementwise", "len": n, "inputs": 1, "expression": {"kind": "input", "binding": 0}}
+    kernel = rt.compile(spec)
+    src, dst = rt.resident(jade_hip.fill_values(n, 0x4242, 1.0)), rt.alloc(n)
+    ms, wall = timed(rt, [(kernel, [src, dst])], steps, warmup)
+    for b in (src, dst):
+        b.free()
+    nbytes = 2.0 * n * 4
+    return {"elements": n, "bytes": nbytes, "ms_per_step": ms, "gbps": nbytes / (ms * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, "kernel": kernel.launch["kernel"]}
+
+
+def _read_csv(path):
+    import csv
+
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _find(directory, suffix):
+    for root, _, files in os.walk(directory):
+        for name in files:
+            if name.endswith(suffix):
+                return os.path.join(root, name)
+    return None
+
+
+def _short(name):
+    name = name.replace("jade::hipk::(anonymous namespace)::", "")
+    name = name[len("void "):] if name.startswith("void ") else name
+    return name.split("(")[0] if "(" in name else name
+
+
+def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
+    """Per (kernel, grid) durations from a rocprofv3 --kernel-trace run, plus HBM
+    bytes per launch from --pmc FETCH_SIZE and WRITE_SIZE runs, scaled by what the
+    same counters read for the copy kernel of known size (COPY_ELEMENTS)."""
+    trace = _read_csv(_find(trace_dir, "kernel_trace.csv"))
+    groups = {}
+    for row in trace:
+        key = (_short(row["Kernel_Name"]), int(row["Grid_Size_X"]), int(row["Grid_Size_Y"]),
+               int(row["Grid_Size_Z"]), int(row["Workgroup_Size_X"]))
+        groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    counters = {}
+    for directory, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        if not directory:
+            continue
+        for row in _read_csv(_find(directory, "counter_collection.csv")):
+            if row.get("Counter_Name") != counter:
+                continue
+            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
+            counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
+    lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us |",
+             "|---|---|---|---|---|---|---|"]
+    for key, durations in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        name, gx, gy, gz, wg = key
+        lines.append(f"| {name} | {gx}x{gy}x{gz} | {wg} | {len(durations)} | {np.mean(durations) / 1e3:.2f} | "
+                     f"{np.min(durations) / 1e3:.2f} | {np.max(durations) / 1e3:.2f} |")
+    traffic = {}
+    if counters:
+        copy_key = next((k for k in counters if k[0] == "copy_stream"), None)
+        expected_kib = COPY_ELEMENTS * 4 / 1024.0
+        scale = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            measured = np.mean(counters.get(copy_key, {}).get(counter, [np.nan])) if copy_key else np.nan
+            scale[counter] = expected_kib / measured if measured and np.isfinite(measured) else np.nan
+        lines += ["", f"HBM counter calibration (copy_stream, {COPY_ELEMENTS * 4 / 2**20:.0f} MiB in and out): "
+                      f"scale FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, WRITE_SIZE x{scale['WRITE_SIZE']:.4f}", "",
+                  "| kernel | grid (work-items) | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB/launch |",
+                  "|---|---|---|---|---|---|"]
+        for key, vals in sorted(counters.items()):
+            fetch = np.mean(vals.get("FETCH_SIZE", [np.nan]))
+            write = np.mean(vals.get("WRITE_SIZE", [np.nan]))
+            nbytes = (fetch * scale["FETCH_SIZE"] + write * scale["WRITE_SIZE"]) * 1024.0
+            count = max(len(vals.get("FETCH_SIZE", [])), len(vals.get("WRITE_SIZE", [])))
+            lines.append(f"| {key[0]} | {key[1]} | {count} | {fetch:.0f} | {write:.0f} | {nbytes / 1e6:.1f} |")
+            if np.isfinite(nbytes):
+                traffic[f"{key[0]}@{key[1]}"] = {"bytes_per_launch": nbytes, "fetch_kib": fetch, "write_kib": write}
+    return "\n".join(lines), traffic
+
+
 def cpu_baseline(gemm, attention):
     """The reference's CPU path (FP64 oracle loops) on this host, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -205,9 +307,22 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep"])
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--summarize-rocprof", metavar="TRACE_DIR",
+                    help="print per-kernel tables from a rocprofv3 --kernel-trace output directory and exit")
+    ap.add_argument("--pmc-fetch", metavar="DIR", help="rocprofv3 --pmc FETCH_SIZE output directory")
+    ap.add_argument("--pmc-write", metavar="DIR", help="rocprofv3 --pmc WRITE_SIZE output directory")
+    ap.add_argument("--traffic-out", metavar="JSON", help="write HBM bytes per launch per (kernel, grid)")
     args = ap.parse_args()
+    if args.summarize_rocprof:
+        table, traffic = summarize_rocprof(args.summarize_rocprof, args.pmc_fetch, args.pmc_write)
+        print(table)
+        if args.traffic_out:
+            with open(args.traffic_out, "w") as f:
+                json.dump(traffic, f, indent=1, sort_keys=True)
+                f.write("\n")
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
@@ -244,6 +359,8 @@ def main():
     if wl in ("all", "mlp"):
         log("six-op MLP 4096x1024x2816 ...")
         extra["mlp_4096x1024x2816"] = bench_mlp(rt, 4096, 1024, 2816, K, W)
+    if wl in ("all", "copy"):
+        extra["copy_calibration"] = bench_copy(rt, K, W)
     if wl in ("all", "sweep"):
         sweep = {}
         for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
@@ -255,8 +372,7 @@ def main():
 
     head = gemm or attention
     if head is None:
-        head_name = "softmax" if wl == "softmax" else "mlp"
-        print(json.dumps({"metric": METRIC, "workload": head_name, "extra": extra}))
+        print(json.dumps({"metric": METRIC, "workload": wl, "extra": extra}))
         return
     if gemm is not None:
         flop_per_launch = 2.0 * gemm["m"] * gemm["n"] * gemm["k"]
@@ -283,13 +399,14 @@ def main():
         "config": config,
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-                     "traffic": traffic_from_profiles(head["kernel"])},
+                     "traffic": traffic_from_profiles(
+                         "gemm_f32_mfma" if gemm is not None else "attention_online_mfma", head["launch"])},
     }
     if attention is not None:
         att = {k: v for k, v in attention.items() if not k.startswith("_")}
         att["roofline"] = {"bound": "mfma", "achieved": attention["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                            "unit": "TFLOP/s", "frac": attention["tflops"] / PEAK_FP32_MFMA_TFLOPS,
-                           "traffic": traffic_from_profiles(attention["kernel"])}
+                           "traffic": traffic_from_profiles("attention_online_mfma", attention["launch"])}
         line["attention"] = att
     if not args.no_cpu_baseline and gemm is not None:
         log("cpu baseline ...")

@@ -108,7 +108,15 @@ void destroy(Context *ctx) {
 jade::hipk::LaunchShape launch_shape(const KernelSpec &s) {
     using namespace jade::hipk;
     switch (s.op) {
-        case Op::Elementwise: return elementwise_shape(s.len);
+        case Op::Elementwise: {
+            const auto &e = *s.expression;
+            if (e.kind == jade::Expr::Kind::Input && e.binding == 0) {
+                auto shape = stream_shape(s.len);
+                shape.kernel = "copy_stream";
+                return shape;
+            }
+            return elementwise_shape(s.len);
+        }
         case Op::Axpy:
         case Op::Add:
         case Op::SwiGlu: return stream_shape(s.len);
