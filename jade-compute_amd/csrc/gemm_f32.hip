@@ -4,10 +4,11 @@
 // ragged edges read as zero and masked on store.
 //
 // Design (gfx950, wave64):
-//  * 256-thread workgroup computes a 128x128 tile; each wave owns 64x64 as
-//    2x2 blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane each).
-//  * K advances 32 per stage. A and B stages are double-buffered in LDS with a
-//    register prefetch of the next stage, one barrier per stage.
+//  * A 256-thread workgroup is a 2x2 grid of waves; each wave owns TM x TN
+//    blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per block), so
+//    a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64, 64x128 or 64x64.
+//  * K advances 32 per stage. Stages are double-buffered in LDS with a register
+//    prefetch of the next stage and one barrier per stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
@@ -21,7 +22,12 @@
 //    round-to-nearest VALU adds. A single chained MFMA accumulation over
 //    K = 4096 drifted by ~3.6e-4 absolute on unit-scale inputs, outside the
 //    1e-4 gate; the stage split keeps the long recurrence to K/32 adds.
+//  * Shapes with too few output tiles to fill 256 CUs split K over gridDim.y:
+//    each slice writes a partial product to a workspace and a reduction kernel
+//    sums the slices in slice order (deterministic, no atomics).
 #include "kernels.hpp"
+
+#include <algorithm>
 
 namespace jade {
 namespace hipk {
@@ -30,15 +36,22 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 32;
 constexpr int kThreads = 256;
+constexpr int kBK = 32;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
-constexpr int kLDB = kBN + 4;  // LDS row stride of a B stage (floats)
 constexpr int kGroupM = 8;
-constexpr int kAStage = kBM * kLDA;
-constexpr int kBStage = kBK * kLDB;
-constexpr int kStage = kAStage + kBStage;
-constexpr uint32_t kLdsBytes = 2u * kStage * sizeof(float);
+
+template <int TM, int TN>
+struct Tile {
+    static constexpr int kBM = 64 * TM, kBN = 64 * TN;
+    static constexpr int kLDB = kBN + 4;  // LDS row stride of a B stage (floats)
+    static constexpr int kAStage = kBM * kLDA;
+    static constexpr int kBStage = kBK * kLDB;
+    static constexpr int kStage = kAStage + kBStage;
+    static constexpr int kALoads = kBM * kBK / 4 / kThreads;  // float4 per thread
+    static constexpr int kBLoads = kBK * kBN / 4 / kThreads;
+    static constexpr uint32_t kLdsBytes = 2u * kStage * sizeof(float);
+};
 
 __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
     const int total = tiles_m * tiles_n;
@@ -55,164 +68,266 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
     tn = in_group / group_rows;
 }
 
-// Stage loads: A tile 128x32 and B tile 32x128, four float4 per thread each.
-template <bool VEC>
+// Stage loads: A tile BMx32 (8 float4 per row) and B tile 32xBN; `kend` is
+// the end of this workgroup's K range (K itself unless K is split).
+template <int TM, int TN, bool VEC>
 __device__ inline void load_stage(const float *__restrict__ A, const float *__restrict__ B, int M, int N, int K,
-                                  int m0, int n0, int k0, f32x4 (&ra)[4], f32x4 (&rb)[4]) {
+                                  int kend, int m0, int n0, int k0, f32x4 (&ra)[Tile<TM, TN>::kALoads],
+                                  f32x4 (&rb)[Tile<TM, TN>::kBLoads]) {
+    using T = Tile<TM, TN>;
     const int t = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < T::kALoads; ++i) {
         const int f = t + i * kThreads;
         const int row = f >> 3, col = (f & 7) << 2;
         const int gr = m0 + row, gc = k0 + col;
         if (VEC) {
-            ra[i] = (gr < M && gc < K) ? *reinterpret_cast<const f32x4 *>(A + (size_t)gr * K + gc)
-                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+            ra[i] = (gr < M && gc < kend) ? *reinterpret_cast<const f32x4 *>(A + (size_t)gr * K + gc)
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
             f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (gr < M && gc + e < K) ? A[(size_t)gr * K + gc + e] : 0.f;
+            for (int e = 0; e < 4; ++e) v[e] = (gr < M && gc + e < kend) ? A[(size_t)gr * K + gc + e] : 0.f;
             ra[i] = v;
         }
     }
+    constexpr int kRowF4 = T::kBN / 4;  // float4 per B row
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < T::kBLoads; ++i) {
         const int f = t + i * kThreads;
-        const int row = f >> 5, col = (f & 31) << 2;
+        const int row = f / kRowF4, col = (f % kRowF4) * 4;
         const int gr = k0 + row, gc = n0 + col;
         if (VEC) {
-            rb[i] = (gr < K && gc < N) ? *reinterpret_cast<const f32x4 *>(B + (size_t)gr * N + gc)
-                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+            rb[i] = (gr < kend && gc < N) ? *reinterpret_cast<const f32x4 *>(B + (size_t)gr * N + gc)
+                                          : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
             f32x4 v;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = (gr < K && gc + e < N) ? B[(size_t)gr * N + gc + e] : 0.f;
+            for (int e = 0; e < 4; ++e) v[e] = (gr < kend && gc + e < N) ? B[(size_t)gr * N + gc + e] : 0.f;
             rb[i] = v;
         }
     }
 }
 
-__device__ inline void store_stage(float *stage, const f32x4 (&ra)[4], const f32x4 (&rb)[4]) {
+template <int TM, int TN>
+__device__ inline void store_stage(float *stage, const f32x4 (&ra)[Tile<TM, TN>::kALoads],
+                                   const f32x4 (&rb)[Tile<TM, TN>::kBLoads]) {
+    using T = Tile<TM, TN>;
     const int t = threadIdx.x;
-    float *as = stage, *bs = stage + kAStage;
+    float *as = stage, *bs = stage + T::kAStage;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < T::kALoads; ++i) {
         const int f = t + i * kThreads;
         *reinterpret_cast<f32x4 *>(as + (f >> 3) * kLDA + ((f & 7) << 2)) = ra[i];
     }
+    constexpr int kRowF4 = T::kBN / 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < T::kBLoads; ++i) {
         const int f = t + i * kThreads;
-        *reinterpret_cast<f32x4 *>(bs + (f >> 5) * kLDB + ((f & 31) << 2)) = rb[i];
+        *reinterpret_cast<f32x4 *>(bs + (f / kRowF4) * T::kLDB + (f % kRowF4) * 4) = rb[i];
     }
 }
 
 // One K stage into fresh accumulators; the caller adds the stage sums into the
 // running totals with VALU adds, so the long K recurrence is 1 add per 32 k
 // instead of 16 chained matrix-core accumulations per 32 k.
-__device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f32x16 (&acc)[2][2]) {
+template <int TM, int TN>
+__device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f32x16 (&acc)[TM][TN]) {
+    using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
-    const float *a0p = stage + (wm * 64 + c) * kLDA + 16 * h;
-    const float *a1p = a0p + 32 * kLDA;
-    const float *bp = stage + kAStage + (16 * h) * kLDB + wn * 64 + c;
+    const float *ap = stage + (wm * 32 * TM + c) * kLDA + 16 * h;
+    const float *bp = stage + T::kAStage + (16 * h) * T::kLDB + wn * 32 * TN + c;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const f32x4 a0 = *reinterpret_cast<const f32x4 *>(a0p + 4 * q);
-        const f32x4 a1 = *reinterpret_cast<const f32x4 *>(a1p + 4 * q);
+        f32x4 a[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = *reinterpret_cast<const f32x4 *>(ap + i * 32 * kLDA + 4 * q);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int s = 4 * q + e;
-            const float b0 = bp[s * kLDB];
-            const float b1 = bp[s * kLDB + 32];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[e], b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[e], b1, acc[1][1], 0, 0, 0);
+            float b[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) b[j] = bp[s * T::kLDB + 32 * j];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[j], acc[i][j], 0, 0, 0);
         }
     }
 }
 
-// Two waves per SIMD (LDS allows two 70.6 KB workgroups per CU); the register
-// budget is capped to match so stage and running accumulators both fit.
-template <bool VEC>
+// Two waves per SIMD (LDS allows two workgroups per CU at the largest tile);
+// the register budget is capped to match so stage and running accumulators fit.
+// gridDim.y > 1 splits K into slices of `kchunk` (a multiple of 32); slice z
+// writes C + z*M*N, which is then a workspace the reduction kernel consumes.
+template <int TM, int TN, bool VEC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
-    int tiles_m, int tiles_n) {
-    __shared__ float smem[2 * kStage];
+    int tiles_m, int tiles_n, int kchunk) {
+    using T = Tile<TM, TN>;
+    __shared__ float smem[2 * T::kStage];
     int tm, tn;
     tile_coords(tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int m0 = tm * T::kBM, n0 = tn * T::kBN;
+    const int kbegin = int(blockIdx.y) * kchunk;
+    const int kend = min(K, kbegin + kchunk);
+    float *__restrict__ out = C + size_t(blockIdx.y) * size_t(M) * size_t(N);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    f32x4 ra[4], rb[4];
-    const int nk = (K + kBK - 1) / kBK;
-    load_stage<VEC>(A, B, M, N, K, m0, n0, 0, ra, rb);
-    store_stage(smem, ra, rb);
+    f32x4 ra[T::kALoads], rb[T::kBLoads];
+    const int nk = (kend - kbegin + kBK - 1) / kBK;
+    load_stage<TM, TN, VEC>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb);
+    store_stage<TM, TN>(smem, ra, rb);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * kStage;
-        float *nxt = smem + ((kt + 1) & 1) * kStage;
+        const float *cur = smem + (kt & 1) * T::kStage;
+        float *nxt = smem + ((kt + 1) & 1) * T::kStage;
         const bool more = kt + 1 < nk;
-        if (more) load_stage<VEC>(A, B, M, N, K, m0, n0, (kt + 1) * kBK, ra, rb);
-        f32x16 part[2][2];
-        mma_stage(cur, wm, wn, lane, part);
+        if (more) load_stage<TM, TN, VEC>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb);
+        f32x16 part[TM][TN];
+        mma_stage<TM, TN>(cur, wm, wn, lane, part);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[i][j] += part[i][j];
-        if (more) store_stage(nxt, ra, rb);
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+        if (more) store_stage<TM, TN>(nxt, ra, rb);
         __syncthreads();
     }
 
     const int h = lane >> 5, c = lane & 31;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + c;
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * 32 * TN + j * 32 + c;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (row < M && col < N) C[(size_t)row * N + col] = acc[i][j][v];
+                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (row < M && col < N) out[(size_t)row * N + col] = acc[i][j][v];
             }
         }
     }
 }
 
+// C[i] = sum over slices z (in order) of W[z*MN + i].
+__global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ W, float *__restrict__ C,
+                                                     size_t mn, int slices) {
+    const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
+    if (i >= mn) return;
+    if (i + 4 <= mn && mn % 4 == 0) {
+        f32x4 s = *reinterpret_cast<const f32x4 *>(W + i);
+        for (int z = 1; z < slices; ++z) s += *reinterpret_cast<const f32x4 *>(W + size_t(z) * mn + i);
+        *reinterpret_cast<f32x4 *>(C + i) = s;
+    } else {
+        for (size_t e = i; e < i + 4 && e < mn; ++e) {
+            float s = W[e];
+            for (int z = 1; z < slices; ++z) s += W[size_t(z) * mn + e];
+            C[e] = s;
+        }
+    }
+}
+
+struct Plan {
+    int tm, tn;     // waves' MFMA blocks: tile = (64*tm) x (64*tn)
+    int slices;     // K slices (1 = no split)
+    int kchunk;     // K per slice, a multiple of 32
+    int tiles_m, tiles_n;
+};
+
+constexpr int kTargetGroups = 480;  // about two workgroups per CU on 256 CUs
+constexpr int kMinChunk = 128;
+
+Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
+    auto tiles = [&](int bm, int bn) { return int(((m + bm - 1) / bm) * ((n + bn - 1) / bn)); };
+    const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
+    for (const auto &s : shapes) {
+        if (s[0] != s[1] && (s[0] == 2) != (m >= n)) continue;  // taller tile for taller C
+        const int t = tiles(64 * s[0], 64 * s[1]);
+        if (t >= kTargetGroups || (s[0] == 1 && s[1] == 1)) {
+            Plan p{s[0], s[1], 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 64 * s[0] - 1) / (64 * s[0])),
+                   int((n + 64 * s[1] - 1) / (64 * s[1]))};
+            if (t < kTargetGroups) {
+                const int want = (kTargetGroups + t - 1) / t;
+                const int most = int(k / kMinChunk);
+                p.slices = std::max(1, std::min(want, most));
+                if (p.slices > 1) {
+                    const int chunk = int((k + p.slices - 1) / p.slices);
+                    p.kchunk = ((chunk + kBK - 1) / kBK) * kBK;
+                    p.slices = int((k + p.kchunk - 1) / p.kchunk);
+                }
+            }
+            return p;
+        }
+    }
+    return {1, 1, 1, int(k), 1, 1};
+}
+
+template <int TM, int TN>
+void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
+                 uint32_t m, uint32_t n, uint32_t k) {
+    const dim3 grid(unsigned(p.tiles_m) * unsigned(p.tiles_n), unsigned(p.slices)), block(kThreads);
+    if (vec)
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true>), grid, block, 0, stream, a, b, out, int(m), int(n), int(k),
+                           p.tiles_m, p.tiles_n, p.kchunk);
+    else
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false>), grid, block, 0, stream, a, b, out, int(m), int(n),
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk);
+}
+
 }  // namespace
 
-LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t) {
-    const uint32_t tiles = ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
-    return {"gemm_f32_mfma_128x128x32", {tiles, 1, 1}, {kThreads, 1, 1}, kLdsBytes};
+size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
+    const Plan p = plan_for(m, n, k);
+    return p.slices > 1 ? size_t(p.slices) * m * n * sizeof(float) : 0;
+}
+
+LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
+    const Plan p = plan_for(m, n, k);
+    static const char *names[2][2][2] = {
+        {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
+         {"gemm_f32_mfma_64x128x32", "gemm_f32_mfma_64x128x32_splitk"}},
+        {{"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},
+         {"gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x128x32_splitk"}}};
+    const uint32_t lds = p.tm == 2 ? (p.tn == 2 ? Tile<2, 2>::kLdsBytes : Tile<2, 1>::kLdsBytes)
+                                   : (p.tn == 2 ? Tile<1, 2>::kLdsBytes : Tile<1, 1>::kLdsBytes);
+    return {names[p.tm - 1][p.tn - 1][p.slices > 1 ? 1 : 0],
+            {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
+            {kThreads, 1, 1},
+            lds};
 }
 
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
-                    uint32_t k) {
-    const int tiles_m = int((m + kBM - 1) / kBM), tiles_n = int((n + kBN - 1) / kBN);
+                    uint32_t k, float *workspace) {
+    const Plan p = plan_for(m, n, k);
     const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0;
     const bool vec = aligned && (k % 4 == 0) && (n % 4 == 0);
-    const dim3 grid(unsigned(tiles_m) * unsigned(tiles_n)), block(kThreads);
-    if (vec)
-        hipLaunchKernelGGL(gemm_f32_mfma<true>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), tiles_m,
-                           tiles_n);
-    else
-        hipLaunchKernelGGL(gemm_f32_mfma<false>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), tiles_m,
-                           tiles_n);
+    if (p.slices > 1 && !workspace) return hipErrorInvalidValue;
+    float *out = p.slices > 1 ? workspace : c;
+    if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
+    else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);
+    else if (p.tn == 2) launch_tile<1, 2>(stream, p, vec, a, b, out, m, n, k);
+    else launch_tile<1, 1>(stream, p, vec, a, b, out, m, n, k);
+    hipError_t status = hipGetLastError();
+    if (status != hipSuccess || p.slices == 1) return status;
+    const size_t mn = size_t(m) * n;
+    const unsigned groups = unsigned((mn + 1023) / 1024);
+    hipLaunchKernelGGL(splitk_reduce, dim3(groups), dim3(256), 0, stream, workspace, c, mn, p.slices);
     return hipGetLastError();
 }
 

@@ -21,6 +21,7 @@ struct Plan {
     int m = 0, n = 0, k = 0, device = 0;
     size_t a_len = 0, b_len = 0, c_len = 0;
     float *a = nullptr, *b = nullptr, *c = nullptr;
+    float *workspace = nullptr;  // split-K partials for small output grids
     hipStream_t stream = nullptr;
     hipEvent_t start = nullptr, stop = nullptr;
     bool uploaded = false, computed = false;
@@ -62,6 +63,7 @@ void cleanup(Plan *p) {
     if (p->a) (void)hipFree(p->a);
     if (p->b) (void)hipFree(p->b);
     if (p->c) (void)hipFree(p->c);
+    if (p->workspace) (void)hipFree(p->workspace);
     if (p->stream) (void)hipStreamDestroy(p->stream);
     delete p;
 }
@@ -109,6 +111,11 @@ extern "C" int jade_corex_create(uint32_t m, uint32_t n, uint32_t k, int device,
         if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(B): %s", hipGetErrorString(status));
         status = hipMalloc(&p->c, p->c_len * sizeof(float));
         if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(C): %s", hipGetErrorString(status));
+        const size_t ws = jade::hipk::gemm_f32_workspace_bytes(m, n, k);
+        if (ws) {
+            status = hipMalloc(&p->workspace, ws);
+            if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(workspace): %s", hipGetErrorString(status));
+        }
         return 0;
     };
     const int rc = initialize();
@@ -152,7 +159,8 @@ extern "C" int jade_corex_run(void *handle, uint32_t iterations, double *elapsed
     auto status = hipEventRecord(p->start, p->stream);
     if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventRecord(start)");
     for (uint32_t i = 0; i < iterations; ++i) {
-        status = jade::hipk::gemm_f32(p->stream, p->a, p->b, p->c, uint32_t(p->m), uint32_t(p->n), uint32_t(p->k));
+        status = jade::hipk::gemm_f32(p->stream, p->a, p->b, p->c, uint32_t(p->m), uint32_t(p->n), uint32_t(p->k),
+                                      p->workspace);
         if (status != hipSuccess) {
             (void)hipStreamSynchronize(p->stream);
             return runtime_error(status, err, cap, "matrix multiplication");

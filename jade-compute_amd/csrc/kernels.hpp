@@ -20,9 +20,12 @@ struct LaunchShape {
 };
 
 // C[m,n] = A[m,k] * B[k,n], packed row-major FP32, FP32 MFMA accumulate.
+// Small output grids split K; they need `gemm_f32_workspace_bytes` of device
+// workspace (0 when the shape does not split), passed as `workspace`.
 LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k);
+size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
-                    uint32_t k);
+                    uint32_t k, float *workspace);
 
 // Flash-style online softmax(Q K^T / sqrt(dim)) V, [heads, seq, dim] contiguous.
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);

@@ -35,6 +35,7 @@ struct Pipeline {
     std::vector<Binding> binds;
     jade::Instr *program = nullptr;  // device copy of an Elementwise program
     uint32_t program_len = 0;
+    float *workspace = nullptr;      // split-K partial products of a small GEMM
     bool copy = false;  // Elementwise whose expression is input0
     int refs = 0;
 };
@@ -87,6 +88,7 @@ int select(Context *ctx, char *err, size_t cap) {
 
 void release_pipeline(Context *ctx, Pipeline *p) {
     if (p->program) (void)hipFree(p->program);
+    if (p->workspace) (void)hipFree(p->workspace);
     ctx->cache.erase(p->canonical);
     ctx->pipelines.erase(p);
     delete p;
@@ -148,7 +150,7 @@ hipError_t launch(const Pipeline &p, hipStream_t st, void *const *b) {
         case Op::Add: return add_f32(st, in(0), in(1), out(2), s.len);
         case Op::SwiGlu: return swiglu_f32(st, in(0), in(1), out(2), s.len);
         case Op::Gemm:
-        case Op::GemmSimd: return gemm_f32(st, in(0), in(1), out(2), s.m, s.n, s.k);
+        case Op::GemmSimd: return gemm_f32(st, in(0), in(1), out(2), s.m, s.n, s.k, p.workspace);
         case Op::AttentionOnline:
             return attention_online_f32(st, in(0), in(1), in(2), out(3), s.heads, s.seq, s.dim, s.causal);
         case Op::AttentionScores:
@@ -492,6 +494,18 @@ extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void 
             if (p->program) (void)hipFree(p->program);
             delete p;
             return hip_fail(status != hipSuccess ? status : sync, err, cap, "upload expression program");
+        }
+    }
+    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd) {
+        const size_t bytes = jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
+        if (bytes) {
+            const auto status = hipMalloc(&p->workspace, bytes);
+            if (status != hipSuccess) {
+                p->workspace = nullptr;
+                delete p;
+                return fail(status == hipErrorOutOfMemory ? 3 : 2, err, cap, "GEMM workspace (%zu bytes): %s", bytes,
+                            hipGetErrorString(status));
+            }
         }
     }
     p->refs = 1;
