@@ -50,8 +50,62 @@ struct Tile {
     static constexpr int kStage = kAStage + kBStage;
     static constexpr int kALoads = kBM * kBK / 4 / kThreads;  // float4 per thread
     static constexpr int kBLoads = kBK * kBN / 4 / kThreads;
+    // Unpadded, XOR-swizzled stage written by LDS-direct loads (interior tiles).
+    static constexpr int kAStageS = kBM * kBK, kBStageS = kBK * kBN, kStageS = kAStageS + kBStageS;
+    static constexpr int kAInst = kAStageS * 4 / 1024 / 4;  // 1 KB LDS-direct loads per wave
+    static constexpr int kBInst = kBStageS * 4 / 1024 / 4;
+    static_assert(kStageS <= kStage, "swizzled stage must fit in the padded stage allocation");
     static constexpr uint32_t kLdsBytes = 2u * kStage * sizeof(float);
 };
+
+// ---- LDS-direct staging --------------------------------------------------
+// global_load_lds_dwordx4 moves 16 bytes per lane straight from global memory
+// into LDS at M0 + lane*16, with no staging registers and no ds_write. It is
+// issued through inline asm with a zero immediate offset: the hardware adds
+// the immediate to both the global and the LDS address. Both bases are
+// wave-uniform and are moved to SGPRs explicitly. The loads are counted by
+// vmcnt, which the caller drains before the barrier that publishes a stage.
+__device__ inline void lds_dma16(const float *base, uint32_t voff, uint32_t lds_addr) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(b));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(b >> 32));
+    const float *ub = reinterpret_cast<const float *>((uint64_t(hi) << 32) | lo);
+    const uint32_t ul = __builtin_amdgcn_readfirstlane(lds_addr);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1\n" ::"v"(voff), "s"(ub), "s"(ul)
+                 : "memory");
+}
+__device__ inline void drain_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+__device__ inline uint32_t lds_address(const void *p) {
+    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
+}
+
+// Swizzled stage layout: row r of a stage is unpadded and its 16-byte chunk j
+// sits at chunk position j ^ (r & 7). Eight consecutive rows read at the same
+// logical chunk (A operands) then touch eight different 16-byte bank groups,
+// and 32 consecutive columns of one row (B operands) stay within one 128-byte
+// group, so both operand reads are free of bank conflicts without padding.
+template <int TM, int TN>
+__device__ inline void issue_stage_dma(const float *__restrict__ A, const float *__restrict__ B, int N, int K,
+                                       int m0, int n0, int k0, uint32_t stage_lds) {
+    using T = Tile<TM, TN>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *abase = A + size_t(m0) * K + k0;
+    const float *bbase = B + size_t(k0) * N + n0;
+    const uint32_t sb = stage_lds + T::kAStageS * 4;
+#pragma unroll
+    for (int i = 0; i < T::kAInst; ++i) {  // eight 128-byte A rows per 1 KB load
+        const int inst = wave * T::kAInst + i;
+        const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ (row & 7);
+        lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
+    }
+    constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
+#pragma unroll
+    for (int i = 0; i < T::kBInst; ++i) {  // BN*4-byte B rows, kRowsPer per 1 KB load
+        const int inst = wave * T::kBInst + i;
+        const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ (row & 7);
+        lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
+    }
+}
 
 __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
     const int total = tiles_m * tiles_n;
@@ -69,8 +123,10 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
 }
 
 // Stage loads: A tile BMx32 (8 float4 per row) and B tile 32xBN; `kend` is
-// the end of this workgroup's K range (K itself unless K is split).
-template <int TM, int TN, bool VEC>
+// the end of this workgroup's K range (K itself unless K is split). GUARD=false
+// is only used for tiles that lie wholly inside A, B and C with a K range that
+// is a whole number of stages, so every access is in bounds without a check.
+template <int TM, int TN, bool VEC, bool GUARD>
 __device__ inline void load_stage(const float *__restrict__ A, const float *__restrict__ B, int M, int N, int K,
                                   int kend, int m0, int n0, int k0, f32x4 (&ra)[Tile<TM, TN>::kALoads],
                                   f32x4 (&rb)[Tile<TM, TN>::kBLoads]) {
@@ -81,7 +137,9 @@ __device__ inline void load_stage(const float *__restrict__ A, const float *__re
         const int f = t + i * kThreads;
         const int row = f >> 3, col = (f & 7) << 2;
         const int gr = m0 + row, gc = k0 + col;
-        if (VEC) {
+        if (VEC && !GUARD) {
+            ra[i] = *reinterpret_cast<const f32x4 *>(A + (size_t)gr * K + gc);
+        } else if (VEC) {
             ra[i] = (gr < M && gc < kend) ? *reinterpret_cast<const f32x4 *>(A + (size_t)gr * K + gc)
                                           : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
@@ -97,7 +155,9 @@ __device__ inline void load_stage(const float *__restrict__ A, const float *__re
         const int f = t + i * kThreads;
         const int row = f / kRowF4, col = (f % kRowF4) * 4;
         const int gr = k0 + row, gc = n0 + col;
-        if (VEC) {
+        if (VEC && !GUARD) {
+            rb[i] = *reinterpret_cast<const f32x4 *>(B + (size_t)gr * N + gc);
+        } else if (VEC) {
             rb[i] = (gr < kend && gc < N) ? *reinterpret_cast<const f32x4 *>(B + (size_t)gr * N + gc)
                                           : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
@@ -163,11 +223,109 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
     }
 }
 
+// mma_stage over the swizzled layout.
+template <int TM, int TN>
+__device__ inline void mma_stage_swz(const float *stage, int wm, int wn, int lane, f32x16 (&acc)[TM][TN]) {
+    using T = Tile<TM, TN>;
+    const int h = lane >> 5, c = lane & 31;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        f32x4 a[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = wm * 32 * TM + i * 32 + c, chunk = 4 * h + q;
+            a[i] = *reinterpret_cast<const f32x4 *>(stage + row * kBK + ((chunk ^ (row & 7)) << 2));
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int krow = 16 * h + 4 * q + e;
+            float b[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = wn * 32 * TN + j * 32 + c;
+                b[j] = stage[T::kAStageS + krow * T::kBN + (((col >> 2) ^ (krow & 7)) << 2) + (col & 3)];
+            }
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
+// The K loop for interior tiles: LDS-direct loads of stage kt+1 run while the
+// matrix cores consume stage kt; each wave drains its own loads, then one
+// barrier publishes the stage and retires the buffer the next loads overwrite.
+template <int TM, int TN>
+__device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
+                                  int K, int kbegin, int kend, int m0, int n0, int wm, int wn, int lane,
+                                  f32x16 (&acc)[TM][TN]) {
+    using T = Tile<TM, TN>;
+    const uint32_t lds0 = lds_address(smem);
+    const int nk = (kend - kbegin) / kBK;
+    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin, lds0);
+    drain_vmem();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const float *cur = smem + (kt & 1) * T::kStageS;
+        if (kt + 1 < nk)
+            issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin + (kt + 1) * kBK,
+                                    lds0 + uint32_t(((kt + 1) & 1) * T::kStageS * 4));
+        f32x16 part[TM][TN];
+        mma_stage_swz<TM, TN>(cur, wm, wn, lane, part);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+        drain_vmem();
+        __syncthreads();
+    }
+}
+
+// The K loop of one workgroup: prefetch stage kt+1 into registers while the
+// matrix cores consume stage kt from LDS, then publish it with one barrier.
+template <int TM, int TN, bool VEC, bool GUARD>
+__device__ inline void k_loop(const float *__restrict__ A, const float *__restrict__ B, float *smem, int M, int N,
+                              int K, int kbegin, int kend, int m0, int n0, int wm, int wn, int lane,
+                              f32x16 (&acc)[TM][TN]) {
+    using T = Tile<TM, TN>;
+    f32x4 ra[T::kALoads], rb[T::kBLoads];
+    const int nk = (kend - kbegin + kBK - 1) / kBK;
+    load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb);
+    store_stage<TM, TN>(smem, ra, rb);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const float *cur = smem + (kt & 1) * T::kStage;
+        float *nxt = smem + ((kt + 1) & 1) * T::kStage;
+        const bool more = kt + 1 < nk;
+        if (more) load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb);
+        f32x16 part[TM][TN];
+        mma_stage<TM, TN>(cur, wm, wn, lane, part);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+        if (more) store_stage<TM, TN>(nxt, ra, rb);
+        __syncthreads();
+    }
+}
+
 // Two waves per SIMD (LDS allows two workgroups per CU at the largest tile);
 // the register budget is capped to match so stage and running accumulators fit.
 // gridDim.y > 1 splits K into slices of `kchunk` (a multiple of 32); slice z
 // writes C + z*M*N, which is then a workspace the reduction kernel consumes.
-template <int TM, int TN, bool VEC>
+// PATH kDmaOnly: every tile of the launch is interior and 16-byte aligned, so
+// only the LDS-direct loop is compiled in (fewer registers, tighter code).
+enum Path { kMixed = 0, kDmaOnly = 1 };
+
+template <int TM, int TN, bool VEC, int PATH>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
     int tiles_m, int tiles_n, int kchunk) {
@@ -190,25 +348,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-    f32x4 ra[T::kALoads], rb[T::kBLoads];
-    const int nk = (kend - kbegin + kBK - 1) / kBK;
-    load_stage<TM, TN, VEC>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb);
-    store_stage<TM, TN>(smem, ra, rb);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * T::kStage;
-        float *nxt = smem + ((kt + 1) & 1) * T::kStage;
-        const bool more = kt + 1 < nk;
-        if (more) load_stage<TM, TN, VEC>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb);
-        f32x16 part[TM][TN];
-        mma_stage<TM, TN>(cur, wm, wn, lane, part);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-        if (more) store_stage<TM, TN>(nxt, ra, rb);
-        __syncthreads();
-    }
+    // Interior tiles with 16-byte rows stream through LDS-direct loads; edge
+    // tiles and unaligned shapes take the guarded, register-staged path.
+    const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && (kend - kbegin) % kBK == 0;
+    if (PATH == kDmaOnly || (VEC && interior))
+        k_loop_dma<TM, TN>(A, B, smem, N, K, kbegin, kend, m0, n0, wm, wn, lane, acc);
+    else
+        k_loop<TM, TN, VEC, true>(A, B, smem, M, N, K, kbegin, kend, m0, n0, wm, wn, lane, acc);
 
     const int h = lane >> 5, c = lane & 31;
 #pragma unroll
@@ -219,7 +365,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (row < M && col < N) out[(size_t)row * N + col] = acc[i][j][v];
+                if (PATH == kDmaOnly || (row < M && col < N)) out[(size_t)row * N + col] = acc[i][j][v];
             }
         }
     }
@@ -282,11 +428,16 @@ template <int TM, int TN>
 void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
                  uint32_t m, uint32_t n, uint32_t k) {
     const dim3 grid(unsigned(p.tiles_m) * unsigned(p.tiles_n), unsigned(p.slices)), block(kThreads);
-    if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true>), grid, block, 0, stream, a, b, out, int(m), int(n), int(k),
-                           p.tiles_m, p.tiles_n, p.kchunk);
+    const bool all_interior = vec && m % (64 * TM) == 0 && n % (64 * TN) == 0 && p.kchunk % kBK == 0 &&
+                              k % uint32_t(p.kchunk) % kBK == 0;
+    if (all_interior)
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly>), grid, block, 0, stream, a, b, out, int(m),
+                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk);
+    else if (vec)
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false>), grid, block, 0, stream, a, b, out, int(m), int(n),
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
                            int(k), p.tiles_m, p.tiles_n, p.kchunk);
 }
 
