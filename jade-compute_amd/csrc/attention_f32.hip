@@ -19,8 +19,14 @@
 // so the longest causal rows of every head dispatch first, and all blocks of a
 // head share one XCD (workgroups go round-robin over 8 XCDs by linear id). A
 // wave skips 32-key sub-tiles that lie wholly above its causal diagonal.
+//
+// Grids too small to fill the chip (fewer blocks than CUs) split each block's
+// key tiles over gridDim.z slices. A slice writes its unnormalised O, running
+// max and normaliser to a workspace, and attention_combine merges the slices:
+// O = sum_z 2^(m_z - M) O_z / sum_z 2^(m_z - M) l_z with M = max_z m_z.
 #include "kernels.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace jade {
@@ -91,12 +97,17 @@ __device__ inline void store_kv(float *stage, const f32x4 (&pk)[AttnShape<DP, NW
     }
 }
 
-template <int DP, int NW, bool CAUSAL, bool VEC>
+// SPLIT: this block covers key tiles [z*T/Z, (z+1)*T/Z) of its T tiles (z =
+// blockIdx.z, Z = gridDim.z) and writes partial results: unnormalised O rows to
+// `O + z*rows*dim` and (running max, normaliser) to `ml[z*rows + row]`, where
+// rows = heads*seq. A slice whose keys all lie above a query's diagonal leaves
+// (-inf, 0) and a zero row for it.
+template <int DP, int NW, bool CAUSAL, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__restrict__ Q,
                                                                  const float *__restrict__ K,
                                                                  const float *__restrict__ V,
-                                                                 float *__restrict__ O, int seq, int dim,
-                                                                 float qscale) {
+                                                                 float *__restrict__ O, float2 *__restrict__ ml,
+                                                                 int seq, int dim, float qscale) {
     using S = AttnShape<DP, NW>;
     constexpr int HALF = DP / 2;
     constexpr int LD = S::kLD;
@@ -111,10 +122,21 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
 
     // Q^T operand: lane half h holds dims [h*HALF, h*HALF + HALF) of query qi.
     float qreg[HALF];
+    if (VEC) {
 #pragma unroll
-    for (int s = 0; s < HALF; ++s) {
-        const int d = h * HALF + s;
-        qreg[s] = (qi < seq && d < dim) ? Q[base + size_t(qi) * dim + d] * qscale : 0.f;
+        for (int s4 = 0; s4 < HALF / 4; ++s4) {
+            const int d = h * HALF + 4 * s4;
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
+            if (qi < seq && d < dim) x = *reinterpret_cast<const f32x4 *>(Q + base + size_t(qi) * dim + d);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) qreg[4 * s4 + e] = x[e] * qscale;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < HALF; ++s) {
+            const int d = h * HALF + s;
+            qreg[s] = (qi < seq && d < dim) ? Q[base + size_t(qi) * dim + d] * qscale : 0.f;
+        }
     }
 
     f32x16 acc[DP / 32];
@@ -126,16 +148,23 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
 
     const int kv_end = CAUSAL ? min(seq, qb * S::kBQ + S::kBQ) : seq;
     const int tiles = (kv_end + kBKV - 1) / kBKV;
+    int t_begin = 0, t_end = tiles;
+    if (SPLIT) {
+        t_begin = int(blockIdx.z) * tiles / int(gridDim.z);
+        t_end = (int(blockIdx.z) + 1) * tiles / int(gridDim.z);
+    }
     f32x4 pk[S::kLoads], pv[S::kLoads];
-    load_kv<DP, NW, VEC>(K, V, base, 0, seq, dim, pk, pv);
-    store_kv<DP, NW>(lds, pk, pv);
+    if (t_begin < t_end) {  // block-uniform
+        load_kv<DP, NW, VEC>(K, V, base, t_begin * kBKV, seq, dim, pk, pv);
+        store_kv<DP, NW>(lds, pk, pv);
+    }
     __syncthreads();
 
-    for (int t = 0; t < tiles; ++t) {
+    for (int t = t_begin; t < t_end; ++t) {
         const int kt = t * kBKV;
-        const bool more = t + 1 < tiles;
+        const bool more = t + 1 < t_end;
         if (more) load_kv<DP, NW, VEC>(K, V, base, kt + kBKV, seq, dim, pk, pv);
-        const float *ks = lds + (t & 1) * 2 * S::kTile;
+        const float *ks = lds + ((t - t_begin) & 1) * 2 * S::kTile;
         const float *vs = ks + S::kTile;
         // Sub-tiles of this tile the wave needs: none above its causal diagonal
         // and none wholly past seq. Wave-uniform.
@@ -171,7 +200,10 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                 }
             }
             tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
-            const float next_max = fmaxf(row_max, tile_max);
+            float next_max = fmaxf(row_max, tile_max);
+            // A slice that starts past key 0 can meet a query with no live key
+            // yet; keep its max finite so the weights below are 0, not NaN.
+            if (SPLIT && next_max == -INFINITY) next_max = 0.f;
             const float old_weight = __builtin_amdgcn_exp2f(row_max - next_max);
             float tile_sum = 0.f;
 #pragma unroll
@@ -203,13 +235,21 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                 }
             }
         }
-        if (more) store_kv<DP, NW>(lds + ((t + 1) & 1) * 2 * S::kTile, pk, pv);
+        if (more) store_kv<DP, NW>(lds + ((t + 1 - t_begin) & 1) * 2 * S::kTile, pk, pv);
         __syncthreads();
     }
 
     if (qi < seq) {
-        const float inv = 1.0f / row_sum;
+        float inv = 1.0f / row_sum;
         float *orow = O + base + size_t(qi) * dim;
+        if (SPLIT) {
+            const size_t rows = size_t(gridDim.x) * size_t(seq);
+            const size_t row = size_t(blockIdx.x) * size_t(seq) + size_t(qi);
+            // row_sum >= 1 once any key is live (the max key contributes 2^0).
+            if (h == 0) ml[blockIdx.z * rows + row] = make_float2(row_sum == 0.f ? -INFINITY : row_max, row_sum);
+            orow += blockIdx.z * rows * size_t(dim);
+            inv = 1.0f;
+        }
 #pragma unroll
         for (int b = 0; b < DP / 32; ++b) {
 #pragma unroll
@@ -265,20 +305,41 @@ __global__ __launch_bounds__(256) void attention_apply_kernel(const float *__res
     O[(head * seq + query) * size_t(dim) + channel] = sum;
 }
 
-template <int DP, int NW, bool CAUSAL>
-hipError_t launch_online(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                         uint32_t heads, uint32_t seq, uint32_t dim, bool vec) {
-    using S = AttnShape<DP, NW>;
-    const unsigned q_blocks = (seq + S::kBQ - 1) / S::kBQ;
-    const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
-    const dim3 grid(heads, q_blocks), block(S::kThreads);
-    if (vec)
-        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, true>), grid, block, 0, stream, q, k, v, out,
-                           int(seq), int(dim), qscale);
-    else
-        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, false>), grid, block, 0, stream, q, k, v, out,
-                           int(seq), int(dim), qscale);
-    return hipGetLastError();
+// Merges the key slices of a split launch: one thread per 4 outputs (VEC) or
+// per output. Split launches have fewer than 256 blocks of 128 queries, so
+// below 2^15 rows of at most 128 floats, and 32-bit indices cover them.
+template <bool VEC>
+__global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ part,
+                                                         const float2 *__restrict__ ml, float *__restrict__ O,
+                                                         uint32_t rows, uint32_t dim, int splits) {
+    constexpr uint32_t W = VEC ? 4 : 1;
+    const uint32_t per_row = dim / W;
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+    if (idx >= rows * per_row) return;
+    const uint32_t row = idx / per_row;
+    const uint32_t total = rows * dim;
+    float top = -INFINITY;
+    for (int z = 0; z < splits; ++z) top = fmaxf(top, ml[z * rows + row].x);
+    f32x4 num = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int z = 0; z < splits; ++z) {
+        const float2 s = ml[z * rows + row];
+        const float w = __builtin_amdgcn_exp2f(s.x - top);
+        den = fmaf(w, s.y, den);
+        if constexpr (VEC) {
+            const f32x4 x = *reinterpret_cast<const f32x4 *>(part + z * total + idx * 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) num[e] = fmaf(w, x[e], num[e]);
+        } else {
+            num[0] = fmaf(w, part[z * total + idx], num[0]);
+        }
+    }
+    if constexpr (VEC) {
+        const f32x4 out = {num[0] / den, num[1] / den, num[2] / den, num[3] / den};
+        *reinterpret_cast<f32x4 *>(O + idx * 4) = out;
+    } else {
+        O[idx] = num[0] / den;
+    }
 }
 
 int padded_dim(uint32_t dim) { return dim <= 32 ? 32 : dim <= 64 ? 64 : 128; }
@@ -290,14 +351,72 @@ int waves_for(uint32_t heads, uint32_t seq) {
     return blocks8 >= 512 ? 8 : 4;
 }
 
+constexpr uint32_t kCUs = 256;
+constexpr uint32_t kMaxSplits = 16;
+
+// Key slices per block: 1 while the grid covers every CU, else enough slices
+// for one block per CU, each slice keeping at least one 64-key tile of the
+// longest rows. Two blocks per CU measured slower: the slices get shorter but
+// the per-CU work is unchanged and the partials double.
+uint32_t splits_for(uint32_t heads, uint32_t seq) {
+    const uint32_t bq = 32u * uint32_t(waves_for(heads, seq));
+    const uint64_t blocks = uint64_t(heads) * ((seq + bq - 1) / bq);
+    if (blocks >= kCUs) return 1;
+    const uint64_t want = (kCUs + blocks - 1) / blocks;
+    const uint64_t tiles = (seq + kBKV - 1) / kBKV;
+    return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>({want, tiles, kMaxSplits})));
+}
+
+// Workspace layout of a split launch: splits*rows*dim partial O floats, then
+// (rounded to 16 bytes) splits*rows float2 (max, normaliser); rows = heads*seq.
+size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t splits) {
+    const size_t n = size_t(splits) * heads * seq * dim;
+    return (n + 3) & ~size_t(3);
+}
+
+template <int DP, int NW, bool CAUSAL, bool SPLIT>
+hipError_t launch_online(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
+                         float2 *ml, uint32_t heads, uint32_t seq, uint32_t dim, uint32_t splits, bool vec) {
+    using S = AttnShape<DP, NW>;
+    const unsigned q_blocks = (seq + S::kBQ - 1) / S::kBQ;
+    const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
+    const dim3 grid(heads, q_blocks, splits), block(S::kThreads);
+    if (vec)
+        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, true, SPLIT>), grid, block, 0, stream, q, k, v,
+                           out, ml, int(seq), int(dim), qscale);
+    else
+        hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, false, SPLIT>), grid, block, 0, stream, q, k, v,
+                           out, ml, int(seq), int(dim), qscale);
+    return hipGetLastError();
+}
+
 template <int DP>
 hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                        uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
+                        float *workspace, uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
+    const uint32_t splits = splits_for(heads, seq);
+    if (splits > 1) {
+        // Split grids are small grids, which always take four-wave blocks.
+        if (waves_for(heads, seq) != 4 || workspace == nullptr) return hipErrorInvalidValue;
+        float *part = workspace;
+        float2 *ml = reinterpret_cast<float2 *>(workspace + split_part_floats(heads, seq, dim, splits));
+        const hipError_t status =
+            causal ? launch_online<DP, 4, true, true>(stream, q, k, v, part, ml, heads, seq, dim, splits, vec)
+                   : launch_online<DP, 4, false, true>(stream, q, k, v, part, ml, heads, seq, dim, splits, vec);
+        if (status != hipSuccess) return status;
+        const uint32_t threads = heads * seq * (vec ? dim / 4 : dim);
+        if (vec)
+            hipLaunchKernelGGL(attention_combine<true>, dim3((threads + 255) / 256), dim3(256), 0, stream, part, ml,
+                               out, heads * seq, dim, int(splits));
+        else
+            hipLaunchKernelGGL(attention_combine<false>, dim3((threads + 255) / 256), dim3(256), 0, stream, part,
+                               ml, out, heads * seq, dim, int(splits));
+        return hipGetLastError();
+    }
     if (waves_for(heads, seq) == 8)
-        return causal ? launch_online<DP, 8, true>(stream, q, k, v, out, heads, seq, dim, vec)
-                      : launch_online<DP, 8, false>(stream, q, k, v, out, heads, seq, dim, vec);
-    return causal ? launch_online<DP, 4, true>(stream, q, k, v, out, heads, seq, dim, vec)
-                  : launch_online<DP, 4, false>(stream, q, k, v, out, heads, seq, dim, vec);
+        return causal ? launch_online<DP, 8, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec)
+                      : launch_online<DP, 8, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec);
+    return causal ? launch_online<DP, 4, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec)
+                  : launch_online<DP, 4, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec);
 }
 
 template <int DP>
@@ -311,24 +430,34 @@ LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, b
     const int dp = padded_dim(dim);
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
+    const uint32_t splits = splits_for(heads, seq);
     const uint32_t lds = dp == 32 ? lds_bytes<32>(nw) : dp == 64 ? lds_bytes<64>(nw) : lds_bytes<128>(nw);
-    return {dp == 32 ? "attention_online_mfma_d32" : dp == 64 ? "attention_online_mfma_d64" : "attention_online_mfma_d128",
-            {heads, (seq + bq - 1) / bq, 1},
+    static const char *const names[2][3] = {
+        {"attention_online_mfma_d32", "attention_online_mfma_d64", "attention_online_mfma_d128"},
+        {"attention_online_mfma_d32_split", "attention_online_mfma_d64_split", "attention_online_mfma_d128_split"}};
+    return {names[splits > 1][dp == 32 ? 0 : dp == 64 ? 1 : 2],
+            {heads, (seq + bq - 1) / bq, splits},
             {uint32_t(nw) * 64u, 1, 1},
             lds};
 }
 
+size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim) {
+    const uint32_t splits = splits_for(heads, seq);
+    if (splits <= 1) return 0;
+    return (split_part_floats(heads, seq, dim, splits) + 2 * size_t(splits) * heads * seq) * sizeof(float);
+}
+
 hipError_t attention_online_f32(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                                uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+                                uint32_t heads, uint32_t seq, uint32_t dim, bool causal, float *workspace) {
     const bool aligned =
         ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
           reinterpret_cast<uintptr_t>(out)) &
          15u) == 0;
     const bool vec = aligned && dim % 4 == 0;
     switch (padded_dim(dim)) {
-        case 32: return dispatch_dim<32>(stream, q, k, v, out, heads, seq, dim, causal, vec);
-        case 64: return dispatch_dim<64>(stream, q, k, v, out, heads, seq, dim, causal, vec);
-        default: return dispatch_dim<128>(stream, q, k, v, out, heads, seq, dim, causal, vec);
+        case 32: return dispatch_dim<32>(stream, q, k, v, out, workspace, heads, seq, dim, causal, vec);
+        case 64: return dispatch_dim<64>(stream, q, k, v, out, workspace, heads, seq, dim, causal, vec);
+        default: return dispatch_dim<128>(stream, q, k, v, out, workspace, heads, seq, dim, causal, vec);
     }
 }
 

@@ -28,9 +28,13 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
                     uint32_t k, float *workspace);
 
 // Flash-style online softmax(Q K^T / sqrt(dim)) V, [heads, seq, dim] contiguous.
+// Grids smaller than the chip split the keys; they need
+// `attention_online_workspace_bytes` of device workspace (0 when the shape
+// does not split), passed as `workspace`.
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
+size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim);
 hipError_t attention_online_f32(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                                uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
+                                uint32_t heads, uint32_t seq, uint32_t dim, bool causal, float *workspace);
 
 // Materialised comparator: scaled scores [heads, seq, seq] (-inf above the
 // causal diagonal) and probabilities x V.

@@ -35,7 +35,7 @@ struct Pipeline {
     std::vector<Binding> binds;
     jade::Instr *program = nullptr;  // device copy of an Elementwise program
     uint32_t program_len = 0;
-    float *workspace = nullptr;      // split-K partial products of a small GEMM
+    float *workspace = nullptr;      // split-K / split-key partials of a small GEMM or attention grid
     bool copy = false;  // Elementwise whose expression is input0
     int refs = 0;
 };
@@ -152,7 +152,8 @@ hipError_t launch(const Pipeline &p, hipStream_t st, void *const *b) {
         case Op::Gemm:
         case Op::GemmSimd: return gemm_f32(st, in(0), in(1), out(2), s.m, s.n, s.k, p.workspace);
         case Op::AttentionOnline:
-            return attention_online_f32(st, in(0), in(1), in(2), out(3), s.heads, s.seq, s.dim, s.causal);
+            return attention_online_f32(st, in(0), in(1), in(2), out(3), s.heads, s.seq, s.dim, s.causal,
+                                        p.workspace);
         case Op::AttentionScores:
             return attention_scores_f32(st, in(0), in(1), out(2), s.heads, s.seq, s.dim, s.causal);
         case Op::AttentionApply: return attention_apply_f32(st, in(0), in(1), out(2), s.heads, s.seq, s.dim);
@@ -496,16 +497,18 @@ extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void 
             return hip_fail(status != hipSuccess ? status : sync, err, cap, "upload expression program");
         }
     }
-    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd) {
-        const size_t bytes = jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
-        if (bytes) {
-            const auto status = hipMalloc(&p->workspace, bytes);
-            if (status != hipSuccess) {
-                p->workspace = nullptr;
-                delete p;
-                return fail(status == hipErrorOutOfMemory ? 3 : 2, err, cap, "GEMM workspace (%zu bytes): %s", bytes,
-                            hipGetErrorString(status));
-            }
+    size_t workspace_bytes = 0;
+    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd)
+        workspace_bytes = jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
+    else if (spec.op == Op::AttentionOnline)
+        workspace_bytes = jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim);
+    if (workspace_bytes) {
+        const auto status = hipMalloc(&p->workspace, workspace_bytes);
+        if (status != hipSuccess) {
+            p->workspace = nullptr;
+            delete p;
+            return fail(status == hipErrorOutOfMemory ? 3 : 2, err, cap, "kernel workspace (%zu bytes): %s",
+                        workspace_bytes, hipGetErrorString(status));
         }
     }
     p->refs = 1;

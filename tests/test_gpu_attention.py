@@ -117,3 +117,31 @@ def test_scale_is_one_over_sqrt_dim(runtime):
     got = run_online(runtime, h, s, d, False, q.reshape(-1), k.reshape(-1), v.reshape(-1)).reshape(s, d)
     assert got[1, 0] == pytest.approx(math.e / (1.0 + math.e), rel=2e-6)
     assert got[0, 0] == pytest.approx(0.5, rel=2e-6)
+
+
+@pytest.mark.parametrize("h,s,d,causal", [(8, 1024, 64, True), (1, 700, 128, True), (2, 513, 32, False),
+                                          (1, 4096, 64, True), (3, 200, 5, True)])
+def test_split_key_grids(runtime, h, s, d, causal):
+    # Grids smaller than the chip split the keys over gridDim.z and merge the
+    # slices; causal slices past a query's diagonal hold no live key for it.
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
+    assert kernel.launch["grid"][2] > 1 and kernel.launch["kernel"].endswith("_split"), kernel.launch
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x4444), orc.normal(n, 0x5555), orc.normal(n, 0x6666)
+    got = run_online(runtime, h, s, d, causal, q, k, v, repeats=2)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_unsplit_four_wave_grid(runtime, causal):
+    h, s, d = 32, 1024, 64  # 256 blocks of 128 queries: no key split
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
+    assert kernel.launch["grid"] == [32, 8, 1] and kernel.launch["block"][0] == 256, kernel.launch
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x7777), orc.normal(n, 0x8888), orc.normal(n, 0x9999)
+    got = run_online(runtime, h, s, d, causal, q, k, v)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
