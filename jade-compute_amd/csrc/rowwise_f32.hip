@@ -1,9 +1,12 @@
-// Row kernels, one row per 64-lane wavefront (four rows per 256-thread block).
+// Row kernels, one row per 64-lane wavefront (four rows per 256-thread block),
+// or for Softmax over rows of 1024..16384 floats, one row per block.
 // RMSNorm follows src/runtime/ir.rs:488-500: inv = rsqrt(sum(x^2)/cols + eps),
 // out = x * inv * w. Softmax follows ir.rs:501-523: max, sum(exp(x - max)),
 // exp(x - max) / sum. When a row fits in registers (cols % 4 == 0 and
 // cols <= 4096) it is read from HBM exactly once and written once; the
-// reductions are wavefront butterflies with no LDS and no barrier.
+// reductions are wavefront butterflies with no LDS and no barrier. Output rows
+// go out as non-temporal vector stores (no L2 allocation for a stream that is
+// not re-read here).
 #include "kernels.hpp"
 
 #include <cmath>
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_cached(const float *__restr
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
         const int idx = lane + 64 * i;
-        if (idx < n4) o4[idx] = v[i] * inv * w4[idx];
+        if (idx < n4) __builtin_nontemporal_store(v[i] * inv * w4[idx], o4 + idx);
     }
 }
 
@@ -108,7 +111,52 @@ __global__ __launch_bounds__(kThreads) void softmax_cached(const float *__restri
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
         const int idx = lane + 64 * i;
-        if (idx < n4) o4[idx] = v[i] * inv;
+        if (idx < n4) __builtin_nontemporal_store(v[i] * inv, o4 + idx);
+    }
+}
+
+// Rows of 1024..16384 floats (cols % 4 == 0): one row per 256-thread block,
+// V float4 per lane, cross-wave reductions through LDS. Spreading a row over
+// four waves keeps each wave's burst at V KiB; a 16 KiB burst per wave (the
+// wave-per-row kernel at 4096 columns) capped the stream at ~5.5 TB/s, where
+// this layout with non-temporal loads and stores reached ~6.2 TB/s.
+template <int V>
+__global__ __launch_bounds__(kThreads) void softmax_block(const float *__restrict__ x, float *__restrict__ out,
+                                                          int cols) {
+    __shared__ float partial[2][kRowsPerBlock];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n4 = cols >> 2;
+    const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + size_t(blockIdx.x) * cols);
+    f32x4 v[V];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int idx = int(threadIdx.x) + kThreads * i;
+        v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    }
+    m = wave_max(m);
+    if (lane == 0) partial[0][wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(partial[0][0], partial[0][1]), fmaxf(partial[0][2], partial[0][3]));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        v[i].x = exp_f32(v[i].x - m);
+        v[i].y = exp_f32(v[i].y - m);
+        v[i].z = exp_f32(v[i].z - m);
+        v[i].w = exp_f32(v[i].w - m);
+        sum += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) partial[1][wave] = sum;
+    __syncthreads();
+    const float inv = 1.0f / ((partial[1][0] + partial[1][1]) + (partial[1][2] + partial[1][3]));
+    f32x4 *o4 = reinterpret_cast<f32x4 *>(out + size_t(blockIdx.x) * cols);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int idx = int(threadIdx.x) + kThreads * i;
+        if (idx < n4) __builtin_nontemporal_store(v[i] * inv, o4 + idx);
     }
 }
 
@@ -147,6 +195,14 @@ int cache_slots(uint32_t cols) {
     return 0;
 }
 
+// float4 per lane of softmax_block for 1024 <= cols <= 16384, cols % 4 == 0;
+// 0 selects the wave-per-row kernels.
+int block_slots(uint32_t cols) {
+    if (cols % 4 != 0 || cols < 1024 || cols > 16384) return 0;
+    const uint32_t per_lane = (cols / 4 + kThreads - 1) / kThreads;
+    return per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : 16;
+}
+
 bool aligned16(const void *a, const void *b, const void *c) {
     return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) &
             15u) == 0;
@@ -176,14 +232,25 @@ hipError_t rms_norm_f32(hipStream_t stream, const float *x, const float *weight,
 }
 
 LaunchShape softmax_shape(uint32_t rows, uint32_t cols) {
+    const int blk = block_slots(cols);
+    if (blk) return {"softmax_block", {rows, 1, 1}, {kThreads, 1, 1}, 2 * kRowsPerBlock * sizeof(float)};
     const int c4 = cache_slots(cols);
     return {c4 ? "softmax_cached" : "softmax_rows", {(rows + kRowsPerBlock - 1) / kRowsPerBlock, 1, 1},
             {kThreads, 1, 1}, 0};
 }
 
 hipError_t softmax_f32(hipStream_t stream, const float *x, float *out, uint32_t rows, uint32_t cols) {
+    const bool aligned = aligned16(x, out, out);
+    switch (aligned ? block_slots(cols) : 0) {
+        case 1: hipLaunchKernelGGL(softmax_block<1>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
+        case 2: hipLaunchKernelGGL(softmax_block<2>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
+        case 4: hipLaunchKernelGGL(softmax_block<4>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
+        case 8: hipLaunchKernelGGL(softmax_block<8>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
+        case 16: hipLaunchKernelGGL(softmax_block<16>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
+        default: break;
+    }
     const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(kThreads);
-    const int c4 = aligned16(x, out, out) ? cache_slots(cols) : 0;
+    const int c4 = aligned ? cache_slots(cols) : 0;
     switch (c4) {
         case 1: hipLaunchKernelGGL(softmax_cached<1>, grid, block, 0, stream, x, out, int(rows), int(cols)); break;
         case 2: hipLaunchKernelGGL(softmax_cached<2>, grid, block, 0, stream, x, out, int(rows), int(cols)); break;

@@ -47,7 +47,8 @@ def test_softmax_config_32768x4096(runtime):
     assert (got >= 0).all()
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 4096), (3, 17), (2, 257), (5, 4100), (4, 6000), (1, 1), (33, 64)])
+@pytest.mark.parametrize("rows,cols", [(64, 4096), (3, 17), (2, 257), (5, 4100), (4, 6000), (1, 1), (33, 64),
+                                       (3, 1024), (2, 1020), (2, 2052), (2, 16384), (1, 16388)])
 def test_softmax_shapes(runtime, rows, cols):
     x = orc.normal(rows * cols, 0x4321, 0.0, 2.0)
     got = run(runtime, {"op": "softmax", "rows": rows, "cols": cols}, [x], rows * cols)
@@ -105,3 +106,11 @@ def test_expression_interpreter_eight_inputs(runtime):
         x = xs[i].astype(np.float64)
         acc = [acc + x, acc * x, np.maximum(acc, x)][i % 3]
     assert_close(got, np.exp(-(acc * 0.125)), 3e-5)
+
+
+@pytest.mark.parametrize("cols,kernel", [(1020, "softmax_cached"), (1024, "softmax_block"), (4096, "softmax_block"),
+                                         (16384, "softmax_block"), (16388, "softmax_rows"), (1025, "softmax_rows")])
+def test_softmax_kernel_choice(runtime, cols, kernel):
+    # Rows of 1024..16384 floats take one block per row; others one wave per row.
+    launch = runtime.compile({"op": "softmax", "rows": 8, "cols": cols}).launch
+    assert launch["kernel"] == kernel, launch
