@@ -368,7 +368,10 @@ def main():
         sweep = {}
         for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
                         (4096, 11008, 4096)):
-            r = bench_gemm(rt, m, n, k, K if m * n * k < 1 << 36 else max(2, K // 2), W)
+            # Short launches get enough warm-up steps to cover the clock ramp
+            # (~40 ms at an assumed 100 TFLOP/s).
+            warm = max(W, int(40e-3 / (2.0 * m * n * k / 100e12)))
+            r = bench_gemm(rt, m, n, k, K if m * n * k < 1 << 36 else max(2, K // 2), warm)
             sweep[f"{m}x{n}x{k}"] = {"ms": r["ms_per_step"], "tflops": r["tflops"],
                                      "frac_mfma": r["tflops"] / PEAK_FP32_MFMA_TFLOPS}
         extra["gemm_sweep"] = sweep

@@ -154,3 +154,17 @@ def test_constant_bits_round_trip():
         d = describe(spec)
         import numpy as np
         assert np.float32(d["spec"]["expression"]["value"]) == np.float32(value)
+
+
+@pytest.mark.parametrize("m,n,k,kernel,grid", [
+    (4096, 4096, 4096, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),
+    (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
+    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32", [256, 1, 1]),
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32", [208, 1, 1]),
+    (512, 512, 512, "gemm_f32_mfma_64x64x32_splitk", [64, 4, 1]),
+    (4096, 11008, 4096, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),
+])
+def test_gemm_launch_plans(m, n, k, kernel, grid):
+    # Largest tile with ~2 workgroups per CU; K split only below half the CUs.
+    launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
+    assert launch["kernel"] == kernel and launch["grid"] == grid, launch
