@@ -21,9 +21,12 @@
 // wave skips 32-key sub-tiles that lie wholly above its causal diagonal.
 //
 // Grids too small to fill the chip (fewer blocks than CUs) split each block's
-// key tiles over gridDim.z slices. A slice writes its unnormalised O, running
-// max and normaliser to a workspace, and attention_combine merges the slices:
+// key tiles into slices of `per` tiles, one block per live slice. A slice writes its
+// unnormalised O, running max and normaliser to a workspace, and
+// attention_combine merges the slices of each row:
 // O = sum_z 2^(m_z - M) O_z / sum_z 2^(m_z - M) l_z with M = max_z m_z.
+// Fixed-size slices give a causal grid's long rows more slices than its short
+// ones, so every live slice costs about the same.
 #include "kernels.hpp"
 
 #include <algorithm>
@@ -97,17 +100,20 @@ __device__ inline void store_kv(float *stage, const f32x4 (&pk)[AttnShape<DP, NW
     }
 }
 
-// SPLIT: this block covers key tiles [z*T/Z, (z+1)*T/Z) of its T tiles (z =
-// blockIdx.z, Z = gridDim.z) and writes partial results: unnormalised O rows to
+// SPLIT: the grid is one block per live slice, longest rows first: blockIdx.x
+// walks query blocks from the last, each contributing heads * ceil(T/per)
+// blocks (T = its key tiles), head fastest. Slice z covers key tiles
+// [z*per, min(T, (z+1)*per)) and writes partial results: unnormalised O rows to
 // `O + z*rows*dim` and (running max, normaliser) to `ml[z*rows + row]`, where
-// rows = heads*seq. A slice whose keys all lie above a query's diagonal leaves
-// (-inf, 0) and a zero row for it.
+// rows = heads*seq. A query with no live key in its slice gets (-inf, 0) and a
+// zero row.
 template <int DP, int NW, bool CAUSAL, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__restrict__ Q,
                                                                  const float *__restrict__ K,
                                                                  const float *__restrict__ V,
                                                                  float *__restrict__ O, float2 *__restrict__ ml,
-                                                                 int seq, int dim, float qscale) {
+                                                                 int seq, int dim, float qscale, int per,
+                                                                 int heads) {
     using S = AttnShape<DP, NW>;
     constexpr int HALF = DP / 2;
     constexpr int LD = S::kLD;
@@ -115,10 +121,30 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = lane >> 5, c = lane & 31;
-    const int qb = int(gridDim.y) - 1 - int(blockIdx.y);  // longest causal rows first
-    const size_t base = size_t(blockIdx.x) * size_t(seq) * size_t(dim);
+    auto tiles_of = [&](int b) { return ((CAUSAL ? min(seq, b * S::kBQ + S::kBQ) : seq) + kBKV - 1) / kBKV; };
+    int head = int(blockIdx.x), qb = int(gridDim.y) - 1 - int(blockIdx.y);  // longest causal rows first
+    int z = 0;
+    if (SPLIT) {  // decode (query block, slice, head) from the live-slice index
+        int rest = int(blockIdx.x);
+        qb = (seq + S::kBQ - 1) / S::kBQ - 1;
+        for (;; --qb) {
+            const int n = heads * ((tiles_of(qb) + per - 1) / per);
+            if (rest < n || qb == 0) break;
+            rest -= n;
+        }
+        head = rest % heads;
+        z = rest / heads;
+    }
+    const size_t base = size_t(head) * size_t(seq) * size_t(dim);
     const int q0 = qb * S::kBQ + wave * 32;
     const int qi = q0 + c;
+
+    const int tiles = tiles_of(qb);
+    int t_begin = 0, t_end = tiles;
+    if (SPLIT) {
+        t_begin = z * per;
+        t_end = min(tiles, t_begin + per);
+    }
 
     // Q^T operand: lane half h holds dims [h*HALF, h*HALF + HALF) of query qi.
     float qreg[HALF];
@@ -146,13 +172,6 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
     float row_max = -INFINITY, row_sum = 0.f;
 
-    const int kv_end = CAUSAL ? min(seq, qb * S::kBQ + S::kBQ) : seq;
-    const int tiles = (kv_end + kBKV - 1) / kBKV;
-    int t_begin = 0, t_end = tiles;
-    if (SPLIT) {
-        t_begin = int(blockIdx.z) * tiles / int(gridDim.z);
-        t_end = (int(blockIdx.z) + 1) * tiles / int(gridDim.z);
-    }
     f32x4 pk[S::kLoads], pv[S::kLoads];
     if (t_begin < t_end) {  // block-uniform
         load_kv<DP, NW, VEC>(K, V, base, t_begin * kBKV, seq, dim, pk, pv);
@@ -243,11 +262,11 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         float inv = 1.0f / row_sum;
         float *orow = O + base + size_t(qi) * dim;
         if (SPLIT) {
-            const size_t rows = size_t(gridDim.x) * size_t(seq);
-            const size_t row = size_t(blockIdx.x) * size_t(seq) + size_t(qi);
+            const size_t rows = size_t(heads) * size_t(seq);
+            const size_t row = size_t(head) * size_t(seq) + size_t(qi);
             // row_sum >= 1 once any key is live (the max key contributes 2^0).
-            if (h == 0) ml[blockIdx.z * rows + row] = make_float2(row_sum == 0.f ? -INFINITY : row_max, row_sum);
-            orow += blockIdx.z * rows * size_t(dim);
+            if (h == 0) ml[z * rows + row] = make_float2(row_sum == 0.f ? -INFINITY : row_max, row_sum);
+            orow += z * rows * size_t(dim);
             inv = 1.0f;
         }
 #pragma unroll
@@ -306,23 +325,30 @@ __global__ __launch_bounds__(256) void attention_apply_kernel(const float *__res
 }
 
 // Merges the key slices of a split launch: one thread per 4 outputs (VEC) or
-// per output. Split launches have fewer than 256 blocks of 128 queries, so
-// below 2^15 rows of at most 128 floats, and 32-bit indices cover them.
+// per output. A row of query block qb has ceil(T(qb)/per) slices, T(qb) being
+// that block's key tiles. Split launches have fewer than 256 blocks of 128
+// queries, so below 2^15 rows of at most 128 floats, and 32-bit indices cover
+// them.
 template <bool VEC>
 __global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ part,
                                                          const float2 *__restrict__ ml, float *__restrict__ O,
-                                                         uint32_t rows, uint32_t dim, int splits) {
+                                                         uint32_t rows, uint32_t seq, uint32_t dim, uint32_t bq,
+                                                         uint32_t per, int causal) {
     constexpr uint32_t W = VEC ? 4 : 1;
     const uint32_t per_row = dim / W;
     const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= rows * per_row) return;
     const uint32_t row = idx / per_row;
+    const uint32_t qb = (row % seq) / bq;
+    const uint32_t kv_end = causal ? min(seq, (qb + 1) * bq) : seq;
+    const uint32_t tiles = (kv_end + kBKV - 1) / kBKV;
+    const int slices = int((tiles + per - 1) / per);
     const uint32_t total = rows * dim;
     float top = -INFINITY;
-    for (int z = 0; z < splits; ++z) top = fmaxf(top, ml[z * rows + row].x);
+    for (int z = 0; z < slices; ++z) top = fmaxf(top, ml[z * rows + row].x);
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
-    for (int z = 0; z < splits; ++z) {
+    for (int z = 0; z < slices; ++z) {
         const float2 s = ml[z * rows + row];
         const float w = __builtin_amdgcn_exp2f(s.x - top);
         den = fmaf(w, s.y, den);
@@ -354,69 +380,83 @@ int waves_for(uint32_t heads, uint32_t seq) {
 constexpr uint32_t kCUs = 256;
 constexpr uint32_t kMaxSplits = 16;
 
-// Key slices per block: 1 while the grid covers every CU, else enough slices
-// for one block per CU, each slice keeping at least one 64-key tile of the
-// longest rows. Two blocks per CU measured slower: the slices get shorter but
-// the per-CU work is unchanged and the partials double.
-uint32_t splits_for(uint32_t heads, uint32_t seq) {
+struct SplitPlan {
+    uint32_t per;     // key tiles per slice
+    uint32_t slices;  // slices of the longest rows (1 = no split)
+    uint32_t live;    // blocks of a split launch: live slices over all rows
+};
+
+// Grids with at least one block per CU run unsplit. Smaller grids take the
+// shortest slices whose live count still fits one block per CU, so the whole
+// launch is one round of equal-cost slices (at most 16 slices per row).
+SplitPlan split_plan(uint32_t heads, uint32_t seq, bool causal) {
     const uint32_t bq = 32u * uint32_t(waves_for(heads, seq));
-    const uint64_t blocks = uint64_t(heads) * ((seq + bq - 1) / bq);
-    if (blocks >= kCUs) return 1;
-    const uint64_t want = (kCUs + blocks - 1) / blocks;
-    const uint64_t tiles = (seq + kBKV - 1) / kBKV;
-    return uint32_t(std::max<uint64_t>(1, std::min<uint64_t>({want, tiles, kMaxSplits})));
+    const uint32_t q_blocks = (seq + bq - 1) / bq;
+    const uint32_t max_tiles = (seq + kBKV - 1) / kBKV;
+    if (uint64_t(heads) * q_blocks >= kCUs) return {max_tiles, 1, 0};
+    for (uint32_t per = (max_tiles + kMaxSplits - 1) / kMaxSplits; per < max_tiles; ++per) {
+        uint64_t live = 0;
+        for (uint32_t qb = 0; qb < q_blocks; ++qb) {
+            const uint32_t kv_end = causal ? std::min(seq, (qb + 1) * bq) : seq;
+            live += ((kv_end + kBKV - 1) / kBKV + per - 1) / per;
+        }
+        if (live * heads <= kCUs) return {per, (max_tiles + per - 1) / per, uint32_t(live * heads)};
+    }
+    return {max_tiles, 1, 0};
 }
 
-// Workspace layout of a split launch: splits*rows*dim partial O floats, then
-// (rounded to 16 bytes) splits*rows float2 (max, normaliser); rows = heads*seq.
-size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t splits) {
-    const size_t n = size_t(splits) * heads * seq * dim;
+// Workspace layout of a split launch: slices*rows*dim partial O floats, then
+// (rounded to 16 bytes) slices*rows float2 (max, normaliser); rows = heads*seq.
+size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t slices) {
+    const size_t n = size_t(slices) * heads * seq * dim;
     return (n + 3) & ~size_t(3);
 }
 
 template <int DP, int NW, bool CAUSAL, bool SPLIT>
 hipError_t launch_online(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                         float2 *ml, uint32_t heads, uint32_t seq, uint32_t dim, uint32_t splits, bool vec) {
+                         float2 *ml, uint32_t heads, uint32_t seq, uint32_t dim, SplitPlan plan, bool vec) {
     using S = AttnShape<DP, NW>;
     const unsigned q_blocks = (seq + S::kBQ - 1) / S::kBQ;
     const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
-    const dim3 grid(heads, q_blocks, splits), block(S::kThreads);
+    const dim3 grid = SPLIT ? dim3(plan.live) : dim3(heads, q_blocks), block(S::kThreads);
     if (vec)
         hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, true, SPLIT>), grid, block, 0, stream, q, k, v,
-                           out, ml, int(seq), int(dim), qscale);
+                           out, ml, int(seq), int(dim), qscale, int(plan.per), int(heads));
     else
         hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, false, SPLIT>), grid, block, 0, stream, q, k, v,
-                           out, ml, int(seq), int(dim), qscale);
+                           out, ml, int(seq), int(dim), qscale, int(plan.per), int(heads));
     return hipGetLastError();
 }
 
 template <int DP>
 hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                         float *workspace, uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
-    const uint32_t splits = splits_for(heads, seq);
-    if (splits > 1) {
+    const SplitPlan plan = split_plan(heads, seq, causal);
+    if (plan.slices > 1) {
         // Split grids are small grids, which always take four-wave blocks.
         if (waves_for(heads, seq) != 4 || workspace == nullptr) return hipErrorInvalidValue;
         float *part = workspace;
-        float2 *ml = reinterpret_cast<float2 *>(workspace + split_part_floats(heads, seq, dim, splits));
+        float2 *ml = reinterpret_cast<float2 *>(workspace + split_part_floats(heads, seq, dim, plan.slices));
         const hipError_t status =
-            causal ? launch_online<DP, 4, true, true>(stream, q, k, v, part, ml, heads, seq, dim, splits, vec)
-                   : launch_online<DP, 4, false, true>(stream, q, k, v, part, ml, heads, seq, dim, splits, vec);
+            causal ? launch_online<DP, 4, true, true>(stream, q, k, v, part, ml, heads, seq, dim, plan, vec)
+                   : launch_online<DP, 4, false, true>(stream, q, k, v, part, ml, heads, seq, dim, plan, vec);
         if (status != hipSuccess) return status;
         const uint32_t threads = heads * seq * (vec ? dim / 4 : dim);
+        const uint32_t bq = AttnShape<DP, 4>::kBQ;
         if (vec)
             hipLaunchKernelGGL(attention_combine<true>, dim3((threads + 255) / 256), dim3(256), 0, stream, part, ml,
-                               out, heads * seq, dim, int(splits));
+                               out, heads * seq, seq, dim, bq, plan.per, causal ? 1 : 0);
         else
             hipLaunchKernelGGL(attention_combine<false>, dim3((threads + 255) / 256), dim3(256), 0, stream, part,
-                               ml, out, heads * seq, dim, int(splits));
+                               ml, out, heads * seq, seq, dim, bq, plan.per, causal ? 1 : 0);
         return hipGetLastError();
     }
+    const SplitPlan whole{plan.per, 1, 0};
     if (waves_for(heads, seq) == 8)
-        return causal ? launch_online<DP, 8, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec)
-                      : launch_online<DP, 8, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec);
-    return causal ? launch_online<DP, 4, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec)
-                  : launch_online<DP, 4, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, 1, vec);
+        return causal ? launch_online<DP, 8, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, whole, vec)
+                      : launch_online<DP, 8, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, whole, vec);
+    return causal ? launch_online<DP, 4, true, false>(stream, q, k, v, out, nullptr, heads, seq, dim, whole, vec)
+                  : launch_online<DP, 4, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, whole, vec);
 }
 
 template <int DP>
@@ -426,23 +466,24 @@ uint32_t lds_bytes(int nw) {
 
 }  // namespace
 
-LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool) {
+LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
     const int dp = padded_dim(dim);
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
-    const uint32_t splits = splits_for(heads, seq);
+    const SplitPlan plan = split_plan(heads, seq, causal);
+    const uint32_t splits = plan.slices;
     const uint32_t lds = dp == 32 ? lds_bytes<32>(nw) : dp == 64 ? lds_bytes<64>(nw) : lds_bytes<128>(nw);
     static const char *const names[2][3] = {
         {"attention_online_mfma_d32", "attention_online_mfma_d64", "attention_online_mfma_d128"},
         {"attention_online_mfma_d32_split", "attention_online_mfma_d64_split", "attention_online_mfma_d128_split"}};
     return {names[splits > 1][dp == 32 ? 0 : dp == 64 ? 1 : 2],
-            {heads, (seq + bq - 1) / bq, splits},
+            {splits > 1 ? plan.live : heads, splits > 1 ? 1u : (seq + bq - 1) / bq, 1},
             {uint32_t(nw) * 64u, 1, 1},
             lds};
 }
 
-size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim) {
-    const uint32_t splits = splits_for(heads, seq);
+size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    const uint32_t splits = split_plan(heads, seq, causal).slices;
     if (splits <= 1) return 0;
     return (split_part_floats(heads, seq, dim, splits) + 2 * size_t(splits) * heads * seq) * sizeof(float);
 }

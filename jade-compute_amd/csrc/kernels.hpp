@@ -32,7 +32,7 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
 // `attention_online_workspace_bytes` of device workspace (0 when the shape
 // does not split), passed as `workspace`.
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
-size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim);
+size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim, bool causal);
 hipError_t attention_online_f32(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                                 uint32_t heads, uint32_t seq, uint32_t dim, bool causal, float *workspace);
 

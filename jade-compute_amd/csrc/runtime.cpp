@@ -501,7 +501,7 @@ extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void 
     if (spec.op == Op::Gemm || spec.op == Op::GemmSimd)
         workspace_bytes = jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
     else if (spec.op == Op::AttentionOnline)
-        workspace_bytes = jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim);
+        workspace_bytes = jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim, spec.causal);
     if (workspace_bytes) {
         const auto status = hipMalloc(&p->workspace, workspace_bytes);
         if (status != hipSuccess) {

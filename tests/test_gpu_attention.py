@@ -122,10 +122,12 @@ def test_scale_is_one_over_sqrt_dim(runtime):
 @pytest.mark.parametrize("h,s,d,causal", [(8, 1024, 64, True), (1, 700, 128, True), (2, 513, 32, False),
                                           (1, 4096, 64, True), (3, 200, 5, True)])
 def test_split_key_grids(runtime, h, s, d, causal):
-    # Grids smaller than the chip split the keys over gridDim.z and merge the
-    # slices; causal slices past a query's diagonal hold no live key for it.
+    # Grids smaller than the chip split the keys into slices (one block per
+    # live slice) and merge them; a causal slice can hold no live key for some
+    # of its queries.
     kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
-    assert kernel.launch["grid"][2] > 1 and kernel.launch["kernel"].endswith("_split"), kernel.launch
+    launch = kernel.launch
+    assert launch["kernel"].endswith("_split") and launch["grid"][0] > h and launch["grid"][1] == 1, launch
     n = h * s * d
     q, k, v = orc.normal(n, 0x4444), orc.normal(n, 0x5555), orc.normal(n, 0x6666)
     got = run_online(runtime, h, s, d, causal, q, k, v, repeats=2)
