@@ -197,12 +197,16 @@ def _read_csv(path):
         return list(csv.DictReader(f))
 
 
-def _find(directory, suffix):
+def _find_all(directory, suffix):
+    found = []
     for root, _, files in os.walk(directory):
-        for name in files:
-            if name.endswith(suffix):
-                return os.path.join(root, name)
-    return None
+        found += [os.path.join(root, name) for name in files if name.endswith(suffix)]
+    return sorted(found)
+
+
+def _find(directory, suffix):
+    found = _find_all(directory, suffix)
+    return found[0] if found else None
 
 
 def _short(name):
@@ -225,11 +229,14 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
     for directory, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
         if not directory:
             continue
-        for row in _read_csv(_find(directory, "counter_collection.csv")):
-            if row.get("Counter_Name") != counter:
-                continue
-            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
-            counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
+        # One counter_collection.csv per profiled run; a directory may hold
+        # several runs (one per workload).
+        for path in _find_all(directory, "counter_collection.csv"):
+            for row in _read_csv(path):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
+                counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
     lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us |",
              "|---|---|---|---|---|---|---|"]
     for key, durations in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
