@@ -382,6 +382,117 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
 }
 
+// ---- 256x256 tile, eight waves of 128x64 ---------------------------------
+// For grids of whole 256x256 tiles that fill the CUs in whole rounds. One
+// 512-thread workgroup per CU (two 64 KiB stages), waves 2 (M) x 4 (N), each
+// wave 4x2 MFMA blocks. A stage's B operands for both column blocks are read
+// once (32 registers), then each row block runs two 16-deep MFMA chains into
+// fresh accumulators and folds them into the running sums, so the per-stage
+// accumulation is the same two-level scheme as the smaller tiles (bit-identical
+// results) while only two blocks' partial sums are live. Per stage each wave
+// issues 128 MFMAs against 16 ds_read_b128 and 16 ds_read2_b32, against 64
+// MFMAs per 8 + 16 for the 64x64 wave tile. Interior tiles only: M and N
+// multiples of 256, K a multiple of 32, 16-byte aligned rows.
+namespace big {
+constexpr int kBM = 256, kBN = 256, kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kAStage = kBM * kBK, kBStage = kBK * kBN, kStage = kAStage + kBStage;  // floats
+constexpr int kAInst = kAStage * 4 / 1024 / kWaves, kBInst = kBStage * 4 / 1024 / kWaves;
+constexpr uint32_t kLdsBytes = 2u * kStage * sizeof(float);
+static_assert(kAInst * kWaves * 8 == kBM && kBInst * kWaves == kBK, "stage must split evenly over the waves");
+
+__device__ inline void issue_stage(const float *__restrict__ A, const float *__restrict__ B, int N, int K, int m0,
+                                   int n0, int k0, uint32_t stage_lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const float *abase = A + size_t(m0) * K + k0;
+    const float *bbase = B + size_t(k0) * N + n0;
+#pragma unroll
+    for (int i = 0; i < kAInst; ++i) {  // eight 128-byte A rows per 1 KiB load
+        const int inst = wave * kAInst + i;
+        const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
+        lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < kBInst; ++i) {  // one 1 KiB B row per load
+        const int row = wave * kBInst + i, j = lane ^ swz_b(row);
+        lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), stage_lds + kAStage * 4 + row * 1024);
+    }
+}
+}  // namespace big
+
+__global__ __launch_bounds__(big::kThreads) void gemm_f32_mfma_256(const float *__restrict__ A,
+                                                                   const float *__restrict__ B,
+                                                                   float *__restrict__ C, int M, int N, int K,
+                                                                   int tiles_m, int tiles_n) {
+    using namespace big;
+    __shared__ float smem[2 * kStage];
+    int tm, tn;
+    tile_coords(tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * kBM, n0 = tn * kBN;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 2, wn = wave & 3;  // wave tile: rows [wm*128, +128), columns [wn*64, +64)
+    const int h = lane >> 5, c = lane & 31;
+    const uint32_t lds0 = lds_address(smem);
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    const int nk = K / kBK;
+    issue_stage(A, B, N, K, m0, n0, 0, lds0);
+    drain_vmem();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const float *stage = smem + (kt & 1) * kStage;
+        if (kt + 1 < nk) issue_stage(A, B, N, K, m0, n0, (kt + 1) * kBK, lds0 + uint32_t(((kt + 1) & 1) * kStage * 4));
+        float b[2][16];  // k-steps 16h + s of this lane's two columns
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = wn * 64 + j * 32 + c;
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int krow = 16 * h + s;
+                b[j][s] = stage[kAStage + krow * kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = wm * 128 + i * 32 + c;
+            f32x4 a[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                a[q] = *reinterpret_cast<const f32x4 *>(stage + row * kBK + (((4 * h + q) ^ swz_a(row)) << 2));
+            f32x16 p0, p1;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                p0[v] = 0.f;
+                p1[v] = 0.f;
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                p0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b[0][s], p0, 0, 0, 0);
+                p1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s >> 2][s & 3], b[1][s], p1, 0, 0, 0);
+            }
+            acc[i][0] += p0;
+            acc[i][1] += p1;
+        }
+        drain_vmem();
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + c;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                C[size_t(row) * N + col] = acc[i][j][v];
+            }
+        }
+}
+
 // C[i] = sum over slices z (in order) of W[z*MN + i].
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ W, float *__restrict__ C,
                                                      size_t mn, int slices) {
@@ -405,6 +516,7 @@ struct Plan {
     int slices;     // K slices (1 = no split)
     int kchunk;     // K per slice, a multiple of 32
     int tiles_m, tiles_n;
+    bool big;       // 256x256 eight-wave tile (tiles_m/tiles_n count 256x256 tiles)
 };
 
 constexpr int kTargetGroups = 480;  // about two workgroups per CU on 256 CUs
@@ -417,7 +529,22 @@ constexpr int kMinChunk = 128;
 // of the CUs: on MI355X, 1024^3 ran at 83 TFLOP/s unsplit (256 workgroups) and
 // 74 split in two, and 512^3 at 28 split in four against 20 unsplit.
 
+constexpr int kCUs = 256;
+
+// The 256x256 tile runs one workgroup per CU; it is taken when its grid fills
+// the CUs in whole rounds to within 6%. Measured on MI355X: 4096^3 (256 tiles)
+// 135.9 against 127.2 TFLOP/s and 8192x8192x4096 (1024) 136.4 against 128.5,
+// but 4096x11008x4096 (688 tiles, 2.69 rounds) 121.8 against 125.4.
+bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
+    if (m % big::kBM != 0 || n % big::kBN != 0 || k % kBK != 0 || k == 0) return false;
+    const uint64_t t = uint64_t(m / big::kBM) * (n / big::kBN);
+    const uint64_t rounds = (t + kCUs - 1) / kCUs;
+    return t >= uint64_t(kCUs) && t * 100 >= rounds * kCUs * 94;
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
+    if (big_fits(m, n, k))
+        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true};
     auto tiles = [&](int bm, int bn) { return int(((m + bm - 1) / bm) * ((n + bn - 1) / bn)); };
     const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
     for (const auto &s : shapes) {
@@ -425,7 +552,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const int t = tiles(64 * s[0], 64 * s[1]);
         if (t >= kTargetGroups || (s[0] == 1 && s[1] == 1)) {
             Plan p{s[0], s[1], 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 64 * s[0] - 1) / (64 * s[0])),
-                   int((n + 64 * s[1] - 1) / (64 * s[1]))};
+                   int((n + 64 * s[1] - 1) / (64 * s[1])), false};
             if (t < kSplitBelow) {
                 const int want = (kSplitTarget + t - 1) / t;
                 const int most = int(k / kMinChunk);
@@ -439,7 +566,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
             return p;
         }
     }
-    return {1, 1, 1, int(k), 1, 1};
+    return {1, 1, 1, int(k), 1, 1, false};
 }
 
 template <int TM, int TN>
@@ -468,6 +595,9 @@ size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 
 LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
+    if (p.big)
+        return {"gemm_f32_mfma_256x256x32", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {big::kThreads, 1, 1},
+                big::kLdsBytes};
     static const char *names[2][2][2] = {
         {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
          {"gemm_f32_mfma_64x128x32", "gemm_f32_mfma_64x128x32_splitk"}},
@@ -487,6 +617,18 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
     const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0;
     const bool vec = aligned && (k % 4 == 0) && (n % 4 == 0);
     if (p.slices > 1 && !workspace) return hipErrorInvalidValue;
+    if (p.big) {
+        if (vec) {
+            hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.tiles_m * p.tiles_n)), dim3(big::kThreads), 0,
+                               stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n);
+            return hipGetLastError();
+        }
+        // Unaligned pointers: the 128x128 register-staged path (no split: the
+        // grid is large).
+        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false};
+        launch_tile<2, 2>(stream, q, false, a, b, c, m, n, k);
+        return hipGetLastError();
+    }
     float *out = p.slices > 1 ? workspace : c;
     if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);

@@ -111,6 +111,17 @@ def test_edge_masking_shapes(runtime, m, n, k):
     gate(got, m, n, k, a, b)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 32), (4096, 4096, 96), (8192, 8192, 256)])
+def test_big_tile_shapes(runtime, m, n, k):
+    # The 256x256 eight-wave kernel: one stage, an odd stage count, four rounds.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == "gemm_f32_mfma_256x256x32", kernel.launch
+    a = orc.values(m * k, 0x77, 1.0)
+    b = orc.values(k * n, 0x88, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b)
+
+
 def test_gemm_plan_abi_bench_flow():
     # src/main.rs:281-310 driving src/corex.rs through native/jade_corex.h.
     m = n = k = 512

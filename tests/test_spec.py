@@ -157,7 +157,9 @@ def test_constant_bits_round_trip():
 
 
 @pytest.mark.parametrize("m,n,k,kernel,grid", [
-    (4096, 4096, 4096, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),
+    (4096, 4096, 4096, "gemm_f32_mfma_256x256x32", [256, 1, 1]),
+    (8192, 8192, 256, "gemm_f32_mfma_256x256x32", [1024, 1, 1]),
+    (4096, 4096, 4112, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # K not a multiple of 32
     (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32", [256, 1, 1]),
     (1000, 777, 513, "gemm_f32_mfma_64x64x32", [208, 1, 1]),
@@ -165,6 +167,7 @@ def test_constant_bits_round_trip():
     (4096, 11008, 4096, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
-    # Largest tile with ~2 workgroups per CU; K split only below half the CUs.
+    # 256x256 when whole 256x256 tiles fill the CUs in whole rounds; else the
+    # largest tile with ~2 workgroups per CU; K split only below half the CUs.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
     assert launch["kernel"] == kernel and launch["grid"] == grid, launch
