@@ -113,12 +113,16 @@ __device__ inline void issue_stage_dma(const float *__restrict__ A, const float 
     }
 }
 
-__device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
-    const int total = tiles_m * tiles_n;
-    const int bid = blockIdx.x;
-    const int per = total / 8, rem = total % 8;
+// Position of block `bid` among `count` when each XCD (blocks go round-robin
+// over the 8 XCDs by id) owns a contiguous range of positions.
+__device__ inline int xcd_order(int bid, int count) {
+    const int per = count / 8, rem = count % 8;
     const int xcd = bid % 8, idx = bid / 8;
-    const int logical = xcd * per + min(xcd, rem) + idx;
+    return xcd * per + min(xcd, rem) + idx;
+}
+
+// Grouped tile order: kGroupM tile rows at a time, column-major inside a group.
+__device__ inline void grouped_tile(int logical, int tiles_m, int tiles_n, int &tm, int &tn) {
     const int group_span = kGroupM * tiles_n;
     const int group = logical / group_span;
     const int first_m = group * kGroupM;
@@ -126,6 +130,10 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
     const int in_group = logical - group * group_span;
     tm = first_m + in_group % group_rows;
     tn = in_group / group_rows;
+}
+
+__device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
+    grouped_tile(xcd_order(int(blockIdx.x), tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // Stage loads: A tile BMx32 (8 float4 per row) and B tile 32xBN; `kend` is
@@ -336,14 +344,26 @@ __device__ inline void k_loop(const float *__restrict__ A, const float *__restri
 // only the LDS-direct loop is compiled in (fewer registers, tighter code).
 enum Path { kMixed = 0, kDmaOnly = 1 };
 
+// tail_base >= 0: the launch covers the 256x256 tiles [tail_base, tail_base +
+// gridDim.x / 4) of the grouped order over a tiles_m x tiles_n grid of 256x256
+// tiles, four 128x128 workgroups each (the remainder after the 256x256 kernel's
+// whole rounds).
 template <int TM, int TN, bool VEC, int PATH>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
-    int tiles_m, int tiles_n, int kchunk) {
+    int tiles_m, int tiles_n, int kchunk, int tail_base) {
     using T = Tile<TM, TN>;
     __shared__ float smem[2 * T::kStage];
     int tm, tn;
-    tile_coords(tiles_m, tiles_n, tm, tn);
+    if (tail_base >= 0) {
+        const int pos = xcd_order(int(blockIdx.x), int(gridDim.x));
+        int bm, bn;
+        grouped_tile(tail_base + pos / 4, tiles_m, tiles_n, bm, bn);
+        tm = 2 * bm + ((pos >> 1) & 1);
+        tn = 2 * bn + (pos & 1);
+    } else {
+        tile_coords(tiles_m, tiles_n, tm, tn);
+    }
     const int m0 = tm * T::kBM, n0 = tn * T::kBN;
     const int kbegin = int(blockIdx.y) * kchunk;
     const int kend = min(K, kbegin + kchunk);
@@ -383,8 +403,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 }
 
 // ---- 256x256 tile, eight waves of 128x64 ---------------------------------
-// For grids of whole 256x256 tiles that fill the CUs in whole rounds. One
-// 512-thread workgroup per CU (two 64 KiB stages), waves 2 (M) x 4 (N), each
+// Runs the whole rounds (256 tiles each) of a grid of 256x256 tiles; the
+// remainder goes to the 128x128 kernel in tail mode. One 512-thread workgroup
+// per CU (two 64 KiB stages), waves 2 (M) x 4 (N), each
 // wave 4x2 MFMA blocks. A stage's B operands for both column blocks are read
 // once (32 registers), then each row block runs two 16-deep MFMA chains into
 // fresh accumulators and folds them into the running sums, so the per-stage
@@ -425,8 +446,8 @@ __global__ __launch_bounds__(big::kThreads) void gemm_f32_mfma_256(const float *
                                                                    int tiles_m, int tiles_n) {
     using namespace big;
     __shared__ float smem[2 * kStage];
-    int tm, tn;
-    tile_coords(tiles_m, tiles_n, tm, tn);
+    int tm, tn;  // the launch covers the first gridDim.x tiles of the grouped order
+    grouped_tile(xcd_order(int(blockIdx.x), int(gridDim.x)), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * kBM, n0 = tn * kBN;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave >> 2, wn = wave & 3;  // wave tile: rows [wm*128, +128), columns [wn*64, +64)
@@ -517,6 +538,7 @@ struct Plan {
     int kchunk;     // K per slice, a multiple of 32
     int tiles_m, tiles_n;
     bool big;       // 256x256 eight-wave tile (tiles_m/tiles_n count 256x256 tiles)
+    int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
 };
 
 constexpr int kTargetGroups = 480;  // about two workgroups per CU on 256 CUs
@@ -531,20 +553,23 @@ constexpr int kMinChunk = 128;
 
 constexpr int kCUs = 256;
 
-// The 256x256 tile runs one workgroup per CU; it is taken when its grid fills
-// the CUs in whole rounds to within 6%. Measured on MI355X: 4096^3 (256 tiles)
-// 135.9 against 127.2 TFLOP/s and 8192x8192x4096 (1024) 136.4 against 128.5,
-// but 4096x11008x4096 (688 tiles, 2.69 rounds) 121.8 against 125.4.
+// The 256x256 tile runs one workgroup per CU, so it takes the whole rounds of
+// 256 tiles of a grid of 256x256 tiles; the rest of the grid (a partial round)
+// runs as 128x128 tiles, two workgroups per CU. Measured on MI355X with the
+// 256x256 kernel alone: 4096^3 (256 tiles) 135.9 against 127.2 TFLOP/s for
+// 128x128, 8192x8192x4096 (1024) 136.4 against 128.5, but 4096x11008x4096
+// (688 tiles, 2.69 rounds) 121.8 against 125.4: a partial round costs a whole
+// one.
 bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     if (m % big::kBM != 0 || n % big::kBN != 0 || k % kBK != 0 || k == 0) return false;
-    const uint64_t t = uint64_t(m / big::kBM) * (n / big::kBN);
-    const uint64_t rounds = (t + kCUs - 1) / kCUs;
-    return t >= uint64_t(kCUs) && t * 100 >= rounds * kCUs * 94;
+    return uint64_t(m / big::kBM) * (n / big::kBN) >= uint64_t(kCUs);
 }
 
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
-    if (big_fits(m, n, k))
-        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true};
+    if (big_fits(m, n, k)) {
+        const int tiles = int((m / big::kBM) * (n / big::kBN));
+        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs};
+    }
     auto tiles = [&](int bm, int bn) { return int(((m + bm - 1) / bm) * ((n + bn - 1) / bn)); };
     const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
     for (const auto &s : shapes) {
@@ -552,7 +577,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const int t = tiles(64 * s[0], 64 * s[1]);
         if (t >= kTargetGroups || (s[0] == 1 && s[1] == 1)) {
             Plan p{s[0], s[1], 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 64 * s[0] - 1) / (64 * s[0])),
-                   int((n + 64 * s[1] - 1) / (64 * s[1])), false};
+                   int((n + 64 * s[1] - 1) / (64 * s[1])), false, 0};
             if (t < kSplitBelow) {
                 const int want = (kSplitTarget + t - 1) / t;
                 const int most = int(k / kMinChunk);
@@ -566,7 +591,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
             return p;
         }
     }
-    return {1, 1, 1, int(k), 1, 1, false};
+    return {1, 1, 1, int(k), 1, 1, false, 0};
 }
 
 template <int TM, int TN>
@@ -577,13 +602,13 @@ void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, co
                               k % uint32_t(p.kchunk) % kBK == 0;
     if (all_interior)
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly>), grid, block, 0, stream, a, b, out, int(m),
-                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk);
+                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
     else if (vec)
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk);
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
     else
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk);
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
 }
 
 }  // namespace
@@ -595,8 +620,10 @@ size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 
 LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    if (p.big)
-        return {"gemm_f32_mfma_256x256x32", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {big::kThreads, 1, 1},
+    if (p.big)  // the first launch; a partial last round follows as 128x128 tiles
+        return {p.big_full < p.tiles_m * p.tiles_n ? "gemm_f32_mfma_256x256x32_tail128" : "gemm_f32_mfma_256x256x32",
+                {uint32_t(p.big_full), 1, 1},
+                {big::kThreads, 1, 1},
                 big::kLdsBytes};
     static const char *names[2][2][2] = {
         {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
@@ -619,8 +646,12 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
     if (p.slices > 1 && !workspace) return hipErrorInvalidValue;
     if (p.big) {
         if (vec) {
-            hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.tiles_m * p.tiles_n)), dim3(big::kThreads), 0,
-                               stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n);
+            hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.big_full)), dim3(big::kThreads), 0, stream, a, b, c,
+                               int(m), int(n), int(k), p.tiles_m, p.tiles_n);
+            const int tail = p.tiles_m * p.tiles_n - p.big_full;
+            if (tail > 0)
+                hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), dim3(unsigned(4 * tail)), dim3(kThreads), 0,
+                                   stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full);
             return hipGetLastError();
         }
         // Unaligned pointers: the 128x128 register-staged path (no split: the

@@ -164,10 +164,11 @@ def test_constant_bits_round_trip():
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32", [256, 1, 1]),
     (1000, 777, 513, "gemm_f32_mfma_64x64x32", [208, 1, 1]),
     (512, 512, 512, "gemm_f32_mfma_64x64x32_splitk", [64, 4, 1]),
-    (4096, 11008, 4096, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),
+    (4096, 11008, 4096, "gemm_f32_mfma_256x256x32_tail128", [512, 1, 1]),  # 688 tiles: 2 rounds + 176 as 128x128
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
-    # 256x256 when whole 256x256 tiles fill the CUs in whole rounds; else the
-    # largest tile with ~2 workgroups per CU; K split only below half the CUs.
+    # 256x256 for the whole rounds of a grid of >= 256 such tiles (the rest as
+    # 128x128); else the largest tile with ~2 workgroups per CU; K split only
+    # below half the CUs.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
     assert launch["kernel"] == kernel and launch["grid"] == grid, launch
