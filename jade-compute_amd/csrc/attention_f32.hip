@@ -40,6 +40,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBKV = 64;  // keys per LDS tile (two 32-key sub-tiles)
+constexpr uint32_t kMaxSplits = 16;  // key slices per row of a split launch, at most
 constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
 
 template <int DP, int NW>
@@ -329,7 +330,7 @@ __global__ __launch_bounds__(256) void attention_apply_kernel(const float *__res
 // that block's key tiles. Split launches have fewer than 256 blocks of 128
 // queries, so below 2^15 rows of at most 128 floats, and 32-bit indices cover
 // them.
-template <bool VEC>
+template <bool VEC, int MAXZ>
 __global__ __launch_bounds__(256) void attention_combine(const float *__restrict__ part,
                                                          const float2 *__restrict__ ml, float *__restrict__ O,
                                                          uint32_t rows, uint32_t seq, uint32_t dim, uint32_t bq,
@@ -342,23 +343,33 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
     const uint32_t qb = (row % seq) / bq;
     const uint32_t kv_end = causal ? min(seq, (qb + 1) * bq) : seq;
     const uint32_t tiles = (kv_end + kBKV - 1) / kBKV;
-    const int slices = int((tiles + per - 1) / per);
+    const int slices = int((tiles + per - 1) / per);  // 1 <= slices <= MAXZ
     const uint32_t total = rows * dim;
+    // Every slice's loads are issued before any is used (a loop over a
+    // run-time count would wait for each load in turn). Indices past this
+    // row's slices re-read its last slice, in bounds, and get weight 0.
+    float2 s[MAXZ];
+    f32x4 x[MAXZ];
+#pragma unroll
+    for (int z = 0; z < MAXZ; ++z) {
+        const uint32_t zz = uint32_t(min(z, slices - 1));
+        s[z] = ml[zz * rows + row];
+        if constexpr (VEC)
+            x[z] = *reinterpret_cast<const f32x4 *>(part + zz * total + idx * 4);
+        else
+            x[z][0] = part[zz * total + idx];
+    }
     float top = -INFINITY;
-    for (int z = 0; z < slices; ++z) top = fmaxf(top, ml[z * rows + row].x);
+#pragma unroll
+    for (int z = 0; z < MAXZ; ++z) top = fmaxf(top, s[z].x);
     f32x4 num = {0.f, 0.f, 0.f, 0.f};
     float den = 0.f;
-    for (int z = 0; z < slices; ++z) {
-        const float2 s = ml[z * rows + row];
-        const float w = __builtin_amdgcn_exp2f(s.x - top);
-        den = fmaf(w, s.y, den);
-        if constexpr (VEC) {
-            const f32x4 x = *reinterpret_cast<const f32x4 *>(part + z * total + idx * 4);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) num[e] = fmaf(w, x[e], num[e]);
-        } else {
-            num[0] = fmaf(w, part[z * total + idx], num[0]);
-        }
+    for (int z = 0; z < MAXZ; ++z) {
+        const float w = z < slices ? __builtin_amdgcn_exp2f(s[z].x - top) : 0.f;
+        den = fmaf(w, s[z].y, den);
+#pragma unroll
+        for (int e = 0; e < int(W); ++e) num[e] = fmaf(w, x[z][e], num[e]);
     }
     if constexpr (VEC) {
         const f32x4 out = {num[0] / den, num[1] / den, num[2] / den, num[3] / den};
@@ -366,6 +377,23 @@ __global__ __launch_bounds__(256) void attention_combine(const float *__restrict
     } else {
         O[idx] = num[0] / den;
     }
+}
+
+template <bool VEC>
+void launch_combine(hipStream_t stream, const float *part, const float2 *ml, float *out, uint32_t rows, uint32_t seq,
+                    uint32_t dim, uint32_t bq, uint32_t per, uint32_t slices, bool causal) {
+    const uint32_t threads = rows * (VEC ? dim / 4 : dim);
+    const dim3 grid((threads + 255) / 256), block(256);
+    const int c = causal ? 1 : 0;
+    if (slices <= 2)
+        hipLaunchKernelGGL((attention_combine<VEC, 2>), grid, block, 0, stream, part, ml, out, rows, seq, dim, bq, per, c);
+    else if (slices <= 4)
+        hipLaunchKernelGGL((attention_combine<VEC, 4>), grid, block, 0, stream, part, ml, out, rows, seq, dim, bq, per, c);
+    else if (slices <= 8)
+        hipLaunchKernelGGL((attention_combine<VEC, 8>), grid, block, 0, stream, part, ml, out, rows, seq, dim, bq, per, c);
+    else
+        hipLaunchKernelGGL((attention_combine<VEC, 16>), grid, block, 0, stream, part, ml, out, rows, seq, dim, bq, per,
+                           c);
 }
 
 int padded_dim(uint32_t dim) { return dim <= 32 ? 32 : dim <= 64 ? 64 : 128; }
@@ -378,7 +406,6 @@ int waves_for(uint32_t heads, uint32_t seq) {
 }
 
 constexpr uint32_t kCUs = 256;
-constexpr uint32_t kMaxSplits = 16;
 
 struct SplitPlan {
     uint32_t per;     // key tiles per slice
@@ -441,14 +468,11 @@ hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, cons
             causal ? launch_online<DP, 4, true, true>(stream, q, k, v, part, ml, heads, seq, dim, plan, vec)
                    : launch_online<DP, 4, false, true>(stream, q, k, v, part, ml, heads, seq, dim, plan, vec);
         if (status != hipSuccess) return status;
-        const uint32_t threads = heads * seq * (vec ? dim / 4 : dim);
         const uint32_t bq = AttnShape<DP, 4>::kBQ;
         if (vec)
-            hipLaunchKernelGGL(attention_combine<true>, dim3((threads + 255) / 256), dim3(256), 0, stream, part, ml,
-                               out, heads * seq, seq, dim, bq, plan.per, causal ? 1 : 0);
+            launch_combine<true>(stream, part, ml, out, heads * seq, seq, dim, bq, plan.per, plan.slices, causal);
         else
-            hipLaunchKernelGGL(attention_combine<false>, dim3((threads + 255) / 256), dim3(256), 0, stream, part,
-                               ml, out, heads * seq, seq, dim, bq, plan.per, causal ? 1 : 0);
+            launch_combine<false>(stream, part, ml, out, heads * seq, seq, dim, bq, plan.per, plan.slices, causal);
         return hipGetLastError();
     }
     const SplitPlan whole{plan.per, 1, 0};
