@@ -266,6 +266,52 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
     return "\n".join(lines), traffic
 
 
+# Shapes for MFMA-utilisation counter runs: each launch keeps the summed
+# SQ_VALU_MFMA_BUSY_CYCLES below the 2^31 at which the counter saturates, and
+# each exercises one production kernel (256x256, 128x64 and 64x64 GEMM tiles;
+# the split-key, four-wave and eight-wave attention launches).
+MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024))
+MFMA_ATTENTION = ((8, 1024, 64, False), (8, 1024, 64, True), (32, 2048, 64, True), (64, 2048, 128, True))
+SIMDS = 1024  # 256 CUs x 4 SIMDs
+XCDS = 8
+
+
+def bench_mfma_shapes(rt, steps, warmup):
+    out = {}
+    for m, n, k in MFMA_GEMMS:
+        r = bench_gemm(rt, m, n, k, steps, warmup)
+        out[f"gemm {m}x{n}x{k}"] = {"kernel": r["kernel"], "ms": r["ms_per_step"], "tflops": r["tflops"]}
+    for heads, seq, dim, causal in MFMA_ATTENTION:
+        r = bench_attention(rt, heads, seq, dim, causal, steps, warmup)
+        out[f"attention H{heads} S{seq} D{dim} {'causal' if causal else 'noncausal'}"] = {
+            "kernel": r["kernel"], "ms": r["ms_per_step"], "tflops": r["tflops"]}
+    return out
+
+
+def summarize_mfma(directory):
+    """MFMA busy share per (kernel, grid) from a rocprofv3 --pmc run with
+    SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: busy / (GUI cycles per XCD x
+    SIMDs). GRBM_GUI_ACTIVE is summed over the 8 XCDs."""
+    vals = {}
+    for path in _find_all(directory, "counter_collection.csv"):
+        for row in _read_csv(path):
+            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
+            vals.setdefault(key, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    lines = ["| kernel | grid (work-items) | dispatches | GRBM_GUI_ACTIVE / XCD | SQ_VALU_MFMA_BUSY_CYCLES | MFMA busy |",
+             "|---|---|---|---|---|---|"]
+    for key, v in sorted(vals.items()):
+        if "SQ_VALU_MFMA_BUSY_CYCLES" not in v or "GRBM_GUI_ACTIVE" not in v:
+            continue
+        busy = np.median(v["SQ_VALU_MFMA_BUSY_CYCLES"])
+        gui = np.median(v["GRBM_GUI_ACTIVE"]) / XCDS
+        if busy <= 0:
+            continue
+        flag = " (saturated)" if busy >= 2.0 ** 31 else ""
+        lines.append(f"| {key[0]} | {key[1]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | {busy:.4g}{flag} | "
+                     f"{100.0 * busy / (gui * SIMDS):.1f}% |")
+    return "\n".join(lines)
+
+
 def cpu_baseline(gemm, attention):
     """The reference's CPU path (FP64 oracle loops) on this host, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -316,14 +362,20 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep", "copy"])
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep", "copy", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--summarize-rocprof", metavar="TRACE_DIR",
                     help="print per-kernel tables from a rocprofv3 --kernel-trace output directory and exit")
     ap.add_argument("--pmc-fetch", metavar="DIR", help="rocprofv3 --pmc FETCH_SIZE output directory")
     ap.add_argument("--pmc-write", metavar="DIR", help="rocprofv3 --pmc WRITE_SIZE output directory")
     ap.add_argument("--traffic-out", metavar="JSON", help="write HBM bytes per launch per (kernel, grid)")
+    ap.add_argument("--summarize-mfma", metavar="PMC_DIR",
+                    help="print MFMA busy shares from a rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE "
+                         "output directory and exit")
     args = ap.parse_args()
+    if args.summarize_mfma:
+        print(summarize_mfma(args.summarize_mfma))
+        return
     if args.summarize_rocprof:
         table, traffic = summarize_rocprof(args.summarize_rocprof, args.pmc_fetch, args.pmc_write)
         print(table)
@@ -371,6 +423,8 @@ def main():
         extra["mlp_4096x1024x2816"] = bench_mlp(rt, 4096, 1024, 2816, K, W)
     if wl in ("all", "copy"):
         extra["copy_calibration"] = bench_copy(rt, K, W)
+    if wl == "mfma":  # counter runs only; not part of the default line
+        extra["mfma_shapes"] = bench_mfma_shapes(rt, K, W)
     if wl in ("all", "sweep"):
         sweep = {}
         for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
