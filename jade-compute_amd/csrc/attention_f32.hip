@@ -192,12 +192,16 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         if (CAUSAL) subs = kt > q0 + 31 ? 0 : (kt + 32 > q0 + 31 ? 1 : subs);
         if (subs > 0) {
             f32x16 st[2];
+            float tile_max = -INFINITY;
+            // A tile whose 64 keys are all inside seq and at or below every
+            // query of the wave needs no mask (wave-uniform).
+            const bool full = kt + kBKV <= seq && (!CAUSAL || kt + kBKV - 1 <= q0);
+            if (full) {
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) st[sb][v] = sb < subs ? 0.f : -INFINITY;
-                if (sb < subs) {
+                for (int sb = 0; sb < 2; ++sb) {
                     const float *krow = ks + (sb * 32 + c) * LD + h * HALF;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) st[sb][v] = 0.f;
 #pragma unroll
                     for (int s4 = 0; s4 < HALF / 4; ++s4) {
                         const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * s4);
@@ -205,20 +209,39 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                         for (int e = 0; e < 4; ++e)
                             st[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qreg[4 * s4 + e], st[sb], 0, 0, 0);
                     }
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) tile_max = fmaxf(tile_max, st[sb][v]);
+                }
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) st[sb][v] = sb < subs ? 0.f : -INFINITY;
+                    if (sb < subs) {
+                        const float *krow = ks + (sb * 32 + c) * LD + h * HALF;
+#pragma unroll
+                        for (int s4 = 0; s4 < HALF / 4; ++s4) {
+                            const f32x4 a = *reinterpret_cast<const f32x4 *>(krow + 4 * s4);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                st[sb] =
+                                    __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qreg[4 * s4 + e], st[sb], 0, 0, 0);
+                        }
+                    }
+                }
+                // Mask keys past seq and above the causal diagonal.
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int key = kt + sb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                        const bool live = key < seq && (!CAUSAL || key <= qi);
+                        st[sb][v] = live ? st[sb][v] : -INFINITY;
+                        tile_max = fmaxf(tile_max, st[sb][v]);
+                    }
                 }
             }
-            // Mask, then the online max / normaliser update (log2 domain).
-            float tile_max = -INFINITY;
-#pragma unroll
-            for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int key = kt + sb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    const bool live = key < seq && (!CAUSAL || key <= qi);
-                    st[sb][v] = live ? st[sb][v] : -INFINITY;
-                    tile_max = fmaxf(tile_max, st[sb][v]);
-                }
-            }
+            // The online max / normaliser update (log2 domain).
             tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
             float next_max = fmaxf(row_max, tile_max);
             // A slice that starts past key 0 can meet a query with no live key
