@@ -43,6 +43,18 @@ constexpr int kBKV = 64;  // keys per LDS tile (two 32-key sub-tiles)
 constexpr uint32_t kMaxSplits = 16;  // key slices per row of a split launch, at most
 constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
 
+// Max and sum over lanes l and l ^ 32 (the two halves of the wave hold the
+// two key halves of a query's scores). v_permlane32_swap exchanges the halves
+// in the VALU, without the LDS round trip of a cross-half shuffle.
+__device__ inline float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <int DP, int NW>
 struct AttnShape {
     static constexpr int kThreads = NW * 64;
@@ -242,7 +254,7 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                 }
             }
             // The online max / normaliser update (log2 domain).
-            tile_max = fmaxf(tile_max, __shfl_xor(tile_max, 32));
+            tile_max = halves_max(tile_max);
             float next_max = fmaxf(row_max, tile_max);
             // A slice that starts past key 0 can meet a query with no live key
             // yet; keep its max finite so the weights below are 0, not NaN.
@@ -257,7 +269,7 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                     tile_sum += st[sb][v];
                 }
             }
-            tile_sum += __shfl_xor(tile_sum, 32);
+            tile_sum = halves_sum(tile_sum);
             row_sum = row_sum * old_weight + tile_sum;
             row_max = next_max;
 #pragma unroll
