@@ -348,14 +348,33 @@ enum Path { kMixed = 0, kDmaOnly = 1 };
 // gridDim.x / 4) of the grouped order over a tiles_m x tiles_n grid of 256x256
 // tiles, four 128x128 workgroups each (the remainder after the 256x256 kernel's
 // whole rounds).
+// pair: a second, independent product of the same shape in the same launch
+// (pair.tiles > 0): positions [tiles, 2*tiles) of the XCD order compute
+// pair.c = pair.a * pair.b.
+struct PairArgs {
+    const float *a;
+    const float *b;
+    float *c;
+    int tiles;
+};
+
 template <int TM, int TN, bool VEC, int PATH>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
-    int tiles_m, int tiles_n, int kchunk, int tail_base) {
+    int tiles_m, int tiles_n, int kchunk, int tail_base, PairArgs pair) {
     using T = Tile<TM, TN>;
     __shared__ float smem[2 * T::kStage];
     int tm, tn;
-    if (tail_base >= 0) {
+    if (pair.tiles > 0) {
+        int pos = xcd_order(int(blockIdx.x), int(gridDim.x));
+        if (pos >= pair.tiles) {
+            A = pair.a;
+            B = pair.b;
+            C = pair.c;
+            pos -= pair.tiles;
+        }
+        grouped_tile(pos, tiles_m, tiles_n, tm, tn);
+    } else if (tail_base >= 0) {
         const int pos = xcd_order(int(blockIdx.x), int(gridDim.x));
         int bm, bn;
         grouped_tile(tail_base + pos / 4, tiles_m, tiles_n, bm, bn);
@@ -596,19 +615,20 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
 
 template <int TM, int TN>
 void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
-                 uint32_t m, uint32_t n, uint32_t k) {
-    const dim3 grid(unsigned(p.tiles_m) * unsigned(p.tiles_n), unsigned(p.slices)), block(kThreads);
+                 uint32_t m, uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
+    const unsigned groups = unsigned(p.tiles_m) * unsigned(p.tiles_n) * (pair.tiles > 0 ? 2u : 1u);
+    const dim3 grid(groups, unsigned(p.slices)), block(kThreads);
     const bool all_interior = vec && m % (64 * TM) == 0 && n % (64 * TN) == 0 && p.kchunk % kBK == 0 &&
                               k % uint32_t(p.kchunk) % kBK == 0;
     if (all_interior)
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly>), grid, block, 0, stream, a, b, out, int(m),
-                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
+                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
     else if (vec)
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
     else
         hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1);
+                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
 }
 
 }  // namespace
@@ -638,6 +658,26 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
             lds};
 }
 
+bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
+    const Plan p = plan_for(m, n, k);
+    return !p.big && p.slices == 1 && m > 0 && n > 0 && k > 0;
+}
+
+hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
+                         const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k) {
+    const Plan p = plan_for(m, n, k);
+    if (p.big || p.slices != 1) return hipErrorInvalidValue;
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(a0) | reinterpret_cast<uintptr_t>(b0) |
+                           reinterpret_cast<uintptr_t>(a1) | reinterpret_cast<uintptr_t>(b1);
+    const bool vec = (bits & 15u) == 0 && (k % 4 == 0) && (n % 4 == 0);
+    const PairArgs pair{a1, b1, c1, p.tiles_m * p.tiles_n};
+    if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    else if (p.tn == 2) launch_tile<1, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    else launch_tile<1, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    return hipGetLastError();
+}
+
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
                     uint32_t k, float *workspace) {
     const Plan p = plan_for(m, n, k);
@@ -651,7 +691,8 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
             const int tail = p.tiles_m * p.tiles_n - p.big_full;
             if (tail > 0)
                 hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), dim3(unsigned(4 * tail)), dim3(kThreads), 0,
-                                   stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full);
+                                   stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full,
+                                   PairArgs{});
             return hipGetLastError();
         }
         // Unaligned pointers: the 128x128 register-staged path (no split: the

@@ -26,6 +26,12 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k);
 size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
                     uint32_t k, float *workspace);
+// Two independent products of one shape (c0 = a0 b0, c1 = a1 b1) in one
+// launch, for shapes whose plan needs no workspace and no 256x256 tile
+// (gemm_f32_pairable); each output is bit-identical to its own gemm_f32.
+bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k);
+hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
+                         const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k);
 
 // Flash-style online softmax(Q K^T / sqrt(dim)) V, [heads, seq, dim] contiguous.
 // Grids smaller than the chip split the keys; they need

@@ -540,6 +540,23 @@ extern "C" int jr_kernel_describe(void *handle, void *kernel, char *out, size_t 
     return write_text(describe(p->spec), out, out_cap, err, cap);
 }
 
+// Two consecutive jobs run as one paired GEMM launch when both are GEMMs of
+// the same shape whose plan pairs, and neither touches the other's output:
+// job y must not read or write x's C (read-after-write, write-after-write) and
+// x must not read y's C (write-after-read). Each output is then bit-identical
+// to ordered launches.
+static bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
+    const KernelSpec &a = static_cast<Pipeline *>(x.kernel)->spec;
+    const KernelSpec &b = static_cast<Pipeline *>(y.kernel)->spec;
+    auto gemm = [](const KernelSpec &s) { return s.op == Op::Gemm || s.op == Op::GemmSimd; };
+    if (!gemm(a) || !gemm(b) || a.m != b.m || a.n != b.n || a.k != b.k) return false;
+    if (x.buffer_count != 3 || y.buffer_count != 3) return false;
+    if (!jade::hipk::gemm_f32_pairable(a.m, a.n, a.k)) return false;
+    for (int i = 0; i < 3; ++i)
+        if (y.buffers[i] == x.buffers[2] || x.buffers[i] == y.buffers[2]) return false;
+    return true;
+}
+
 extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size_t job_count, uint32_t repeats,
                                      double *gpu_ms, char *err, size_t cap) {
     clear(err, cap);
@@ -572,11 +589,27 @@ extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size
     }
     const int rc = select(ctx, err, cap);
     if (rc) return rc;
+    // Adjacent independent GEMMs of one shape share a launch (pairable()).
+    std::vector<bool> paired(job_count, false);
+    for (size_t j = 0; j + 1 < job_count; ++j)
+        if (!paired[j] && pairable(jobs[j], jobs[j + 1])) paired[j] = true, ++j;
     return timed_sequence(
         ctx, repeats, gpu_ms,
         [&]() -> hipError_t {
             for (size_t j = 0; j < job_count; ++j) {
-                const auto status = launch(*static_cast<Pipeline *>(jobs[j].kernel), ctx->stream, jobs[j].buffers);
+                hipError_t status;
+                if (paired[j]) {
+                    const KernelSpec &s = static_cast<Pipeline *>(jobs[j].kernel)->spec;
+                    void *const *x = jobs[j].buffers;
+                    void *const *y = jobs[j + 1].buffers;
+                    status = jade::hipk::gemm_f32_pair(
+                        ctx->stream, static_cast<const float *>(x[0]), static_cast<const float *>(x[1]),
+                        static_cast<float *>(x[2]), static_cast<const float *>(y[0]), static_cast<const float *>(y[1]),
+                        static_cast<float *>(y[2]), s.m, s.n, s.k);
+                    ++j;
+                } else {
+                    status = launch(*static_cast<Pipeline *>(jobs[j].kernel), ctx->stream, jobs[j].buffers);
+                }
                 if (status != hipSuccess) return status;
             }
             return hipSuccess;

@@ -150,3 +150,50 @@ def test_gemm_plan_abi_bench_flow():
         np.testing.assert_array_equal(plan.download(), out)
     finally:
         plan.close()
+
+
+def _gemm_batch(runtime, jobs_spec, arrays, repeats=1):
+    # jobs_spec: list of (m, n, k, [names of A, B, C]); arrays: name -> host array or element count
+    bufs = {}
+    for name, value in arrays.items():
+        bufs[name] = runtime.resident(value) if isinstance(value, np.ndarray) else runtime.alloc(value)
+    jobs = [(runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}), [bufs[x] for x in names])
+            for m, n, k, names in jobs_spec]
+    runtime.execute(jobs, repeats)
+    out = {name: runtime.download(buf) for name, buf in bufs.items()}
+    for buf in bufs.values():
+        buf.free()
+    return out
+
+
+def test_paired_gemms_match_separate_launches(runtime):
+    # Two independent GEMMs of one shape (the MLP's gate and up projections)
+    # run as one paired launch; each output must equal its own launch bit for bit.
+    m = n = k = 1024
+    a, b0, b1 = orc.values(m * k, 0x31, 1.0), orc.values(k * n, 0x32, 1.0), orc.values(k * n, 0x33, 1.0)
+    both = _gemm_batch(runtime, [(m, n, k, ["a", "b0", "c0"]), (m, n, k, ["a", "b1", "c1"])],
+                       {"a": a, "b0": b0, "b1": b1, "c0": m * n, "c1": m * n})
+    one = _gemm_batch(runtime, [(m, n, k, ["a", "b0", "c0"])], {"a": a, "b0": b0, "c0": m * n})
+    two = _gemm_batch(runtime, [(m, n, k, ["a", "b1", "c1"])], {"a": a, "b1": b1, "c1": m * n})
+    np.testing.assert_array_equal(both["c0"], one["c0"])
+    np.testing.assert_array_equal(both["c1"], two["c1"])
+    gate(both["c1"], m, n, k, a, b1)
+
+
+def test_dependent_gemms_keep_order(runtime):
+    # Read-after-write (c1 = c0 * b) and write-after-read (the second job
+    # overwrites the first job's input) must not share a launch.
+    m = n = k = 1024
+    a, b = orc.values(m * k, 0x41, 1.0), orc.values(k * n, 0x42, 0.03)
+    raw = _gemm_batch(runtime, [(m, n, k, ["a", "b", "c0"]), (m, n, k, ["c0", "b", "c1"])],
+                      {"a": a, "b": b, "c0": m * n, "c1": m * n})
+    c0 = orc.gemm_reference(m, n, k, a, b).astype(np.float32)
+    gate(raw["c0"], m, n, k, a, b)
+    gate(raw["c1"], m, n, k, raw["c0"], b)
+    # war: job 1 reads x, job 2 writes x = a * b; two repeats, so the second
+    # repeat's first job reads the product.
+    war = _gemm_batch(runtime, [(m, n, k, ["x", "b", "c0"]), (m, n, k, ["a", "b", "x"])],
+                      {"x": a.copy(), "a": a, "b": b, "c0": m * n}, repeats=2)
+    gate(war["x"], m, n, k, a, b)
+    gate(war["c0"], m, n, k, war["x"], b)
+    assert np.abs(c0 - war["x"]).max() < 1e-3
