@@ -4,11 +4,16 @@
 // ragged edges read as zero and masked on store.
 //
 // Design (gfx950, wave64):
-//  * A 256-thread workgroup is a 2x2 grid of waves; each wave owns TM x TN
-//    blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per block), so
-//    a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64, 64x128 or 64x64.
-//  * K advances 32 per stage. Stages are double-buffered in LDS with a register
-//    prefetch of the next stage and one barrier per stage.
+//  * Grids of at least 256 whole 256x256 tiles run gemm_f32_mfma_256: one
+//    512-thread workgroup per CU, eight waves of 128x64 (below); a partial last
+//    round of such tiles runs as 128x128 tiles of the kernel below.
+//  * Otherwise a 256-thread workgroup is a 2x2 grid of waves; each wave owns
+//    TM x TN blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per
+//    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64, 64x128
+//    or 64x64. Two independent products of one shape can share a launch.
+//  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
+//    LDS-direct loads (interior tiles) or a register prefetch (edge tiles and
+//    unaligned shapes), with one barrier per stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
