@@ -164,6 +164,17 @@ hipError_t launch(const Pipeline &p, hipStream_t st, void *const *b) {
     return hipErrorInvalidValue;
 }
 
+// Device workspace a pipeline allocates at jr_compile (split-K partial
+// products of small GEMM grids, split-key partial rows of small attention
+// grids); 0 for every other launch.
+size_t workspace_bytes_for(const KernelSpec &spec) {
+    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd)
+        return jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
+    if (spec.op == Op::AttentionOnline)
+        return jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim, spec.causal);
+    return 0;
+}
+
 std::string describe(const KernelSpec &spec) {
     std::string ref_error, hip_error;
     const bool reference_valid = jade::validate(spec, jade::Rules::Reference, ref_error);
@@ -188,8 +199,9 @@ std::string describe(const KernelSpec &spec) {
                std::to_string(shape.grid[2]) + "],\"block\":[" + std::to_string(shape.block[0]) + "," +
                std::to_string(shape.block[1]) + "," + std::to_string(shape.block[2]) +
                "],\"lds_bytes\":" + std::to_string(shape.lds_bytes) + "}";
+        out += ",\"workspace_bytes\":" + std::to_string(workspace_bytes_for(spec));
     } else {
-        out += ",\"launch\":null";
+        out += ",\"launch\":null,\"workspace_bytes\":0";
     }
     return out + "}";
 }
@@ -497,11 +509,7 @@ extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void 
             return hip_fail(status != hipSuccess ? status : sync, err, cap, "upload expression program");
         }
     }
-    size_t workspace_bytes = 0;
-    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd)
-        workspace_bytes = jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
-    else if (spec.op == Op::AttentionOnline)
-        workspace_bytes = jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim, spec.causal);
+    const size_t workspace_bytes = workspace_bytes_for(spec);
     if (workspace_bytes) {
         const auto status = hipMalloc(&p->workspace, workspace_bytes);
         if (status != hipSuccess) {
