@@ -9,8 +9,8 @@
 //    round of such tiles runs as 128x128 tiles of the kernel below.
 //  * Otherwise a 256-thread workgroup is a 2x2 grid of waves; each wave owns
 //    TM x TN blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per
-//    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64, 64x128
-//    or 64x64. Two independent products of one shape can share a launch.
+//    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64 or
+//    64x64. Two independent products of one shape can share a launch.
 //  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
 //    LDS-direct loads (interior tiles) or a register prefetch (edge tiles and
 //    unaligned shapes), with one barrier per stage.
@@ -565,15 +565,22 @@ struct Plan {
     int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
 };
 
-constexpr int kTargetGroups = 480;  // about two workgroups per CU on 256 CUs
-constexpr int kSplitBelow = 128;    // 64x64 grids below half the CUs split K
-constexpr int kSplitTarget = 256;   // ... into about one workgroup per CU
+constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
+constexpr int kMinGroups = 384;    // a tile shape needs ~1.5 workgroups per CU to be considered
+constexpr int kSplitBelow = 128;   // 64x64 grids below half the CUs split K
+constexpr int kSplitTarget = 256;  // ... into about one workgroup per CU
 constexpr int kMinChunk = 128;
 
-// Tile choice: the largest tile whose grid still gives ~two workgroups per CU;
-// else 64x64. K is split only when even the 64x64 grid covers fewer than half
-// of the CUs: on MI355X, 1024^3 ran at 83 TFLOP/s unsplit (256 workgroups) and
-// 74 split in two, and 512^3 at 28 split in four against 20 unsplit.
+// Tile choice among 128x128, 128x64 and 64x64 (128x64 measured at or above
+// 64x128 on the tall and wide shapes tried, so 64x128 is not chosen). Each
+// candidate with at least kMinGroups workgroups scores fill x eff, where
+// fill = groups / (kSlots x rounds) is the busy share of its rounds and eff =
+// 1.00 / 0.97 / 0.90 its throughput on whole rounds. Measured on MI355X:
+// 3072^3 runs 64x64 at 111 TFLOP/s (128x128, whose second round is 12% full:
+// 94); 6144x1024x1024 64x64 109 (128x64: 93); 2500^3 128x128 88 (128x64: 82);
+// 1024x4096x4096 128x64 124 (64x128: 117). Below that, 64x64; K is split only
+// when the 64x64 grid covers fewer than half the CUs: 1024^3 ran at 83 TFLOP/s
+// unsplit and 74 split in two, 512^3 at 28 split in four and 20 unsplit.
 
 constexpr int kCUs = 256;
 
@@ -594,28 +601,37 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
         return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs};
     }
-    auto tiles = [&](int bm, int bn) { return int(((m + bm - 1) / bm) * ((n + bn - 1) / bn)); };
-    const int shapes[4][2] = {{2, 2}, {2, 1}, {1, 2}, {1, 1}};
-    for (const auto &s : shapes) {
-        if (s[0] != s[1] && (s[0] == 2) != (m >= n)) continue;  // taller tile for taller C
-        const int t = tiles(64 * s[0], 64 * s[1]);
-        if (t >= kTargetGroups || (s[0] == 1 && s[1] == 1)) {
-            Plan p{s[0], s[1], 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 64 * s[0] - 1) / (64 * s[0])),
-                   int((n + 64 * s[1] - 1) / (64 * s[1])), false, 0};
-            if (t < kSplitBelow) {
-                const int want = (kSplitTarget + t - 1) / t;
-                const int most = int(k / kMinChunk);
-                p.slices = std::max(1, std::min(want, most));
-                if (p.slices > 1) {
-                    const int chunk = int((k + p.slices - 1) / p.slices);
-                    p.kchunk = ((chunk + kBK - 1) / kBK) * kBK;
-                    p.slices = int((k + p.kchunk - 1) / p.kchunk);
-                }
-            }
-            return p;
+    const int kchunk = int(((k + kBK - 1) / kBK) * kBK);
+    auto grid = [&](int tm, int tn) {
+        return Plan{tm, tn, 1, kchunk, int((m + 64 * tm - 1) / (64 * tm)), int((n + 64 * tn - 1) / (64 * tn)), false,
+                    0};
+    };
+    const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
+    const double eff[3] = {1.00, 0.97, 0.90};
+    int best = -1;
+    double best_score = 0.0;
+    for (int i = 0; i < 3; ++i) {
+        const Plan p = grid(shapes[i][0], shapes[i][1]);
+        const int groups = p.tiles_m * p.tiles_n;
+        if (groups < kMinGroups) continue;
+        const int rounds = (groups + kSlots - 1) / kSlots;
+        const double score = eff[i] * double(groups) / double(kSlots * rounds);
+        if (score > best_score) best = i, best_score = score;
+    }
+    if (best >= 0) return grid(shapes[best][0], shapes[best][1]);
+    Plan p = grid(1, 1);
+    const int t = p.tiles_m * p.tiles_n;
+    if (t < kSplitBelow) {
+        const int want = (kSplitTarget + t - 1) / t;
+        const int most = int(k / kMinChunk);
+        p.slices = std::max(1, std::min(want, most));
+        if (p.slices > 1) {
+            const int chunk = int((k + p.slices - 1) / p.slices);
+            p.kchunk = ((chunk + kBK - 1) / kBK) * kBK;
+            p.slices = int((k + p.kchunk - 1) / p.kchunk);
         }
     }
-    return {1, 1, 1, int(k), 1, 1, false, 0};
+    return p;
 }
 
 template <int TM, int TN>
@@ -650,14 +666,14 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                 {uint32_t(p.big_full), 1, 1},
                 {big::kThreads, 1, 1},
                 big::kLdsBytes};
-    static const char *names[2][2][2] = {
-        {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
-         {"gemm_f32_mfma_64x128x32", "gemm_f32_mfma_64x128x32_splitk"}},
-        {{"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},
-         {"gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x128x32_splitk"}}};
-    const uint32_t lds = p.tm == 2 ? (p.tn == 2 ? Tile<2, 2>::kLdsBytes : Tile<2, 1>::kLdsBytes)
-                                   : (p.tn == 2 ? Tile<1, 2>::kLdsBytes : Tile<1, 1>::kLdsBytes);
-    return {names[p.tm - 1][p.tn - 1][p.slices > 1 ? 1 : 0],
+    // plan_for yields 128x128, 128x64 or 64x64 tiles; only 64x64 grids split K.
+    const int shape = p.tm == 2 ? (p.tn == 2 ? 2 : 1) : 0;
+    static const char *names[3][2] = {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
+                                      {"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},
+                                      {"gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x128x32_splitk"}};
+    static const uint32_t lds_bytes[3] = {Tile<1, 1>::kLdsBytes, Tile<2, 1>::kLdsBytes, Tile<2, 2>::kLdsBytes};
+    const uint32_t lds = lds_bytes[shape];
+    return {names[shape][p.slices > 1 ? 1 : 0],
             {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
             {kThreads, 1, 1},
             lds};
@@ -678,7 +694,6 @@ hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, f
     const PairArgs pair{a1, b1, c1, p.tiles_m * p.tiles_n};
     if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
-    else if (p.tn == 2) launch_tile<1, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else launch_tile<1, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     return hipGetLastError();
 }
@@ -709,7 +724,6 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
     float *out = p.slices > 1 ? workspace : c;
     if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);
-    else if (p.tn == 2) launch_tile<1, 2>(stream, p, vec, a, b, out, m, n, k);
     else launch_tile<1, 1>(stream, p, vec, a, b, out, m, n, k);
     hipError_t status = hipGetLastError();
     if (status != hipSuccess || p.slices == 1) return status;

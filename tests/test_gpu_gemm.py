@@ -101,10 +101,11 @@ def test_config_gemm_llm_shape(runtime):
 
 @pytest.mark.parametrize("m,n,k", [(129, 130, 131), (255, 257, 4), (3, 4100, 7), (4100, 3, 9), (128, 128, 1),
                                    (200, 8, 1000), (100, 200, 1000), (100, 200, 999), (1, 1024, 4096),
-                                   (4097, 65, 300), (65, 4097, 300), (300, 300, 8192)])
+                                   (4097, 65, 300), (65, 4097, 300), (300, 300, 8192), (4000, 4000, 100),
+                                   (4100, 2800, 64), (4100, 2800, 63)])
 def test_edge_masking_shapes(runtime, m, n, k):
-    # Covers every tile shape (128x128, 128x64, 64x128, 64x64) and the split-K
-    # path with ragged and unaligned K slices.
+    # Covers every tile shape (128x128, 128x64, 64x64) with ragged edges, the
+    # unaligned (scalar-load) path and split K with ragged and unaligned K slices.
     a = orc.values(m * k, 0x55, 1.0)
     b = orc.values(k * n, 0x66, 1.0)
     got = run_gemm(runtime, m, n, k, a, b)
