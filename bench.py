@@ -173,6 +173,33 @@ def bench_mlp(rt, batch, width, hidden, steps, warmup):
             "per_op": per}
 
 
+def bench_rows(rt, batch, width, hidden, steps, warmup):
+    """The MLP's bandwidth-bound ops launched one at a time at the MLP shapes,
+    with the MLP's inputs (the counter runs read HBM bytes per kernel)."""
+    x = jade_hip.fill_normal(batch * width, 0x1234)
+    gamma = jade_hip.fill_values(width, 0x7777, 0.5) + np.float32(1.0)
+    gate = jade_hip.fill_normal(batch * hidden, 0x2468)
+    up = jade_hip.fill_normal(batch * hidden, 0x1357)
+    proj = jade_hip.fill_normal(batch * width, 0x9999)
+    cases = [
+        ("rms_norm", {"op": "rms_norm", "rows": batch, "cols": width, "epsilon": 1e-6}, (x, gamma), batch * width,
+         (2.0 * batch * width + width) * 4),
+        ("swiglu", {"op": "swi_glu", "len": batch * hidden}, (gate, up), batch * hidden, 3.0 * batch * hidden * 4),
+        ("add", {"op": "add", "len": batch * width}, (proj, x), batch * width, 3.0 * batch * width * 4),
+    ]
+    out = {}
+    for name, spec, inputs, n_out, nbytes in cases:
+        kernel = rt.compile(spec)
+        bufs = [rt.resident(t) for t in inputs] + [rt.alloc(n_out)]
+        ms, _ = timed(rt, [(kernel, bufs)], steps, warmup)
+        for b in bufs:
+            b.free()
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {"ms": ms, "bytes": nbytes, "gbps": gbps, "frac_hbm": gbps / PEAK_HBM_GBPS,
+                     "kernel": kernel.launch["kernel"]}
+    return out
+
+
 COPY_ELEMENTS = 1 << 26  # 256 MiB read + 256 MiB written per launch
 
 
@@ -362,7 +389,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemm", "attention", "softmax", "mlp", "sweep", "copy", "mfma"])
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--summarize-rocprof", metavar="TRACE_DIR",
                     help="print per-kernel tables from a rocprofv3 --kernel-trace output directory and exit")
@@ -421,6 +448,8 @@ def main():
     if wl in ("all", "mlp"):
         log("six-op MLP 4096x1024x2816 ...")
         extra["mlp_4096x1024x2816"] = bench_mlp(rt, 4096, 1024, 2816, K, W)
+    if wl == "rows":  # counter runs only; the default line times these ops inside the MLP block
+        extra["rows_mlp_shapes"] = bench_rows(rt, 4096, 1024, 2816, K, W)
     if wl in ("all", "copy"):
         extra["copy_calibration"] = bench_copy(rt, K, W)
     if wl == "mfma":  # counter runs only; not part of the default line
