@@ -27,9 +27,12 @@
 //    round-to-nearest VALU adds. A single chained MFMA accumulation over
 //    K = 4096 drifted by ~3.6e-4 absolute on unit-scale inputs, outside the
 //    1e-4 gate; the stage split keeps the long recurrence to K/32 adds.
-//  * Shapes with too few output tiles to fill 256 CUs split K over gridDim.y:
-//    each slice writes a partial product to a workspace and a reduction kernel
-//    sums the slices in slice order (deterministic, no atomics).
+//  * Small grids with aligned A rows and moderate K run gemm_f32_direct: 32x32
+//    tiles whose waves split K, operands loaded straight into registers, one
+//    launch (below).
+//  * Other shapes with too few output tiles to fill 256 CUs split K over
+//    gridDim.y: each slice writes a partial product to a workspace and a
+//    reduction kernel sums the slices in slice order (deterministic, no atomics).
 #include "kernels.hpp"
 
 #include <algorithm>
@@ -538,6 +541,126 @@ __global__ __launch_bounds__(big::kThreads) void gemm_f32_mfma_256(const float *
         }
 }
 
+// ---- Direct-load 32x32 tiles for small grids -------------------------------
+// For products whose 64x64 grid cannot fill the chip, with 16-byte aligned A
+// rows (K % 4 == 0). A workgroup of G waves computes one 32x32 tile of C; wave
+// g sums the 32-deep K slices g, g+G, g+2G, ... Each lane loads its own MFMA
+// operands straight from global memory (L2) into registers: lane (c, h) needs
+// A[row c][16h, 16h+16) of a slice (four 16-byte loads) and B[16h, 16h+16)[col
+// c] (sixteen loads, each coalesced over 32 lanes into one 128-byte row
+// segment). There is no LDS staging and no barrier in the K loop, so three
+// slices (60 loads, inside the 6-bit vmcnt) stay in flight per wave, and the
+// whole product is one launch (the split-K plan needs a second, reducing one).
+//
+// Loads carry no bounds branches, so the compiler waits for exactly the slice
+// it consumes: row, column and k indices are clamped into the matrices. A
+// clamped row of A (or column of B) only reaches rows (columns) of the 32x32
+// product that are never stored; k >= K is zeroed in both operands when the
+// last, partial slice is consumed. At the end waves 1..G-1 leave their sums in
+// LDS and wave 0 adds them in wave order: the result is deterministic. Per
+// element: each slice is a 16-step MFMA chain from zero, added to the wave's
+// running sum.
+namespace direct {
+constexpr int kDepth = 3;  // slices in flight per wave
+
+struct Slice {
+    f32x4 a[4];   // A[row c][k0 + 16h + 4q + e] at a[q][e]
+    float b[16];  // B[k0 + 16h + s][col c] at b[s]
+};
+
+// A 4-float run clamped to start at most at K - 4 stays inside its row.
+__device__ inline void load_slice(const float *__restrict__ A, const float *__restrict__ B, int K, int N,
+                                  size_t arow, int bcol, int k0, int h, Slice &s) {
+    const int kb = k0 + 16 * h;
+    const float *ap = A + arow * K;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s.a[q] = *reinterpret_cast<const f32x4 *>(ap + min(kb + 4 * q, K - 4));
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s.b[e] = B[size_t(min(kb + e, K - 1)) * N + bcol];
+}
+
+// `valid` = K - (k0 + 16h): operand pairs at s >= valid lie past K.
+__device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
+    f32x16 part;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) part[v] = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int i = 4 * q + e;
+            const float a = i < valid ? s.a[q][e] : 0.f, b = i < valid ? s.b[i] : 0.f;
+            part = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, part, 0, 0, 0);
+        }
+    acc += part;
+}
+}  // namespace direct
+
+template <int G>
+__global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
+                                                          float *__restrict__ C, int M, int N, int K, int tiles_m,
+                                                          int tiles_n) {
+    using namespace direct;
+    constexpr int D = kDepth;
+    __shared__ float red[(G > 1 ? G - 1 : 1) * 16 * 64];
+    int tm, tn;
+    tile_coords(tiles_m, tiles_n, tm, tn);
+    const int lane = threadIdx.x & 63;
+    const int g = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave index, uniform
+    const int c = lane & 31, h = lane >> 5;
+    const int row = tm * 32 + c, col = tn * 32 + c;
+    const size_t arow = size_t(min(row, M - 1));
+    const int bcol = min(col, N - 1);
+    const int slices = (K + kBK - 1) / kBK;
+    const int count = g < slices ? (slices - g + G - 1) / G : 0;  // this wave's slices g, g+G, ...
+    // K offset of this wave's j-th slice, clamped to the last slice: loads past
+    // the end re-read an in-range slice and are never consumed.
+    auto slice_k = [&](int j) { return min(g + j * G, slices - 1) * kBK; };
+    auto valid = [&](int j) { return K - slice_k(j) - 16 * h; };
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+    Slice buf[D];
+    if (count > 0) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            load_slice(A, B, K, N, arow, bcol, slice_k(d), h, buf[d]);
+            __builtin_amdgcn_sched_barrier(0);  // loads issued slice by slice
+        }
+        int i = 0;
+        for (; i + D <= count; i += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                mma_slice(buf[d], valid(i + d), acc);
+                load_slice(A, B, K, N, arow, bcol, slice_k(i + d + D), h, buf[d]);
+                // Keep the slices in order: interleaving their independent
+                // MFMA chains would make the first one wait for every load.
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+            if (i + d < count) mma_slice(buf[d], valid(i + d), acc);
+    }
+    if (G > 1) {
+        if (g > 0) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) red[((g - 1) * 16 + v) * 64 + lane] = acc[v];
+        }
+        __syncthreads();
+        if (g != 0) return;
+#pragma unroll
+        for (int w = 1; w < G; ++w)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[v] += red[((w - 1) * 16 + v) * 64 + lane];
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int crow = tm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (crow < M && col < N) C[size_t(crow) * N + col] = acc[v];
+    }
+}
+
 // C[i] = sum over slices z (in order) of W[z*MN + i].
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ W, float *__restrict__ C,
                                                      size_t mn, int slices) {
@@ -563,6 +686,7 @@ struct Plan {
     int tiles_m, tiles_n;
     bool big;       // 256x256 eight-wave tile (tiles_m/tiles_n count 256x256 tiles)
     int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
+    int direct;     // > 0: gemm_f32_direct with this many waves (tiles_m/tiles_n count 32x32 tiles)
 };
 
 constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
@@ -596,15 +720,37 @@ bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     return uint64_t(m / big::kBM) * (n / big::kBN) >= uint64_t(kCUs);
 }
 
+// Direct-load 32x32 tiles (one launch, K split over the waves of a workgroup)
+// for grids of fewer 64x64 tiles than CUs, aligned A rows, at least 64 tiles
+// of 32x32 and at most 16 slices of 32 k per wave: G = 4 waves up to 512 such
+// tiles, else 2, and no more waves than slices. Measured on MI355X against the
+// 64x64 / split-K plans: 512^3 7.4 against 9.6 us, 384^3 6.8 against 7.9,
+// 700^3 14.9 against 16.9, 1024x512x1024 18.1 against 25.4, 1000x777x512 17.7
+// against 21.9. With K = 8192 the split-K plan is 2-3x faster, and unaligned
+// rows (K = 513) cost the direct loads more than the LDS-staged kernel.
+int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
+    if (k % 4 != 0) return 0;
+    const uint64_t t64 = uint64_t((m + 63) / 64) * ((n + 63) / 64);
+    const uint64_t t32 = uint64_t((m + 31) / 32) * ((n + 31) / 32);
+    if (t64 >= uint64_t(kCUs) || t32 < 64) return 0;
+    const uint32_t slices = (k + kBK - 1) / kBK;
+    int g = t32 > 512 ? 2 : 4;
+    if (slices > uint32_t(16 * g)) return 0;
+    while (g > 1 && uint32_t(g) > slices) g /= 2;
+    return g;
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
-        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs};
+        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0};
     }
     const int kchunk = int(((k + kBK - 1) / kBK) * kBK);
+    if (const int g = direct_waves(m, n, k))
+        return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g};
     auto grid = [&](int tm, int tn) {
         return Plan{tm, tn, 1, kchunk, int((m + 64 * tm - 1) / (64 * tm)), int((n + 64 * tn - 1) / (64 * tn)), false,
-                    0};
+                    0, 0};
     };
     const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
     const double eff[3] = {1.00, 0.97, 0.90};
@@ -666,7 +812,15 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                 {uint32_t(p.big_full), 1, 1},
                 {big::kThreads, 1, 1},
                 big::kLdsBytes};
-    // plan_for yields 128x128, 128x64 or 64x64 tiles; only 64x64 grids split K.
+    if (p.direct) {
+        static const char *names[3] = {"gemm_f32_direct_32x32x32_w1", "gemm_f32_direct_32x32x32_w2",
+                                       "gemm_f32_direct_32x32x32_w4"};
+        return {names[p.direct == 4 ? 2 : p.direct - 1],
+                {uint32_t(p.tiles_m * p.tiles_n), 1, 1},
+                {uint32_t(64 * p.direct), 1, 1},
+                uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
+    }
+    // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 grids split K.
     const int shape = p.tm == 2 ? (p.tn == 2 ? 2 : 1) : 0;
     static const char *names[3][2] = {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
                                       {"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},
@@ -681,13 +835,13 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
 
 bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    return !p.big && p.slices == 1 && m > 0 && n > 0 && k > 0;
+    return !p.big && !p.direct && p.slices == 1 && m > 0 && n > 0 && k > 0;
 }
 
 hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
                          const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    if (p.big || p.slices != 1) return hipErrorInvalidValue;
+    if (p.big || p.direct || p.slices != 1) return hipErrorInvalidValue;
     const uintptr_t bits = reinterpret_cast<uintptr_t>(a0) | reinterpret_cast<uintptr_t>(b0) |
                            reinterpret_cast<uintptr_t>(a1) | reinterpret_cast<uintptr_t>(b1);
     const bool vec = (bits & 15u) == 0 && (k % 4 == 0) && (n % 4 == 0);
@@ -717,8 +871,26 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         }
         // Unaligned pointers: the 128x128 register-staged path (no split: the
         // grid is large).
-        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false};
+        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0};
         launch_tile<2, 2>(stream, q, false, a, b, c, m, n, k);
+        return hipGetLastError();
+    }
+    if (p.direct) {
+        const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
+        if ((reinterpret_cast<uintptr_t>(a) & 15u) != 0) {
+            // Unaligned A: the 64x64 register-staged tiles (no split, no workspace).
+            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0};
+            launch_tile<1, 1>(stream, q, false, a, b, c, m, n, k);
+        } else if (p.direct == 4) {
+            hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
+                               p.tiles_n);
+        } else if (p.direct == 2) {
+            hipLaunchKernelGGL(gemm_f32_direct<2>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
+                               p.tiles_n);
+        } else {
+            hipLaunchKernelGGL(gemm_f32_direct<1>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
+                               p.tiles_n);
+        }
         return hipGetLastError();
     }
     float *out = p.slices > 1 ? workspace : c;

@@ -112,6 +112,22 @@ def test_edge_masking_shapes(runtime, m, n, k):
     gate(got, m, n, k, a, b)
 
 
+@pytest.mark.parametrize("m,n,k,waves", [(300, 200, 100, 4), (1000, 777, 512, 2), (512, 512, 2048, 4),
+                                          (257, 255, 36, 2), (255, 257, 4, 1), (96, 700, 1020, 4),
+                                          (700, 700, 700, 4), (2047, 33, 164, 4)])
+def test_direct_tile_shapes(runtime, m, n, k, waves):
+    # The direct-load 32x32 kernel: ragged M and N (clamped rows and columns that
+    # are never stored), a partial last K slice (zeroed past K), one, two and
+    # four waves per tile, and per-wave slice counts that leave 0, 1 or 2 slices
+    # after the last whole round of three in flight.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == f"gemm_f32_direct_32x32x32_w{waves}", kernel.launch
+    a = orc.values(m * k, 0x99, 1.0)
+    b = orc.values(k * n, 0xAA, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    gate(got, m, n, k, a, b)
+
+
 @pytest.mark.parametrize("m,n,k,tail", [(4096, 4096, 32, False), (4096, 4096, 96, False), (8192, 8192, 256, False),
                                          (5120, 5120, 64, True), (6144, 6144, 32, True)])
 def test_big_tile_shapes(runtime, m, n, k, tail):

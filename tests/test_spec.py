@@ -163,7 +163,11 @@ def test_constant_bits_round_trip():
     (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32", [256, 1, 1]),
     (1000, 777, 513, "gemm_f32_mfma_64x64x32", [208, 1, 1]),
-    (512, 512, 512, "gemm_f32_mfma_64x64x32_splitk", [64, 4, 1]),
+    (512, 512, 512, "gemm_f32_direct_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K
+    (1000, 777, 512, "gemm_f32_direct_32x32x32_w2", [800, 1, 1]),  # > 512 32x32 tiles: two waves
+    (255, 257, 4, "gemm_f32_direct_32x32x32_w1", [72, 1, 1]),  # one slice: one wave
+    (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk", [64, 4, 1]),  # 32 slices per wave: split K instead
+    (256, 256, 4096, "gemm_f32_mfma_64x64x32_splitk", [16, 16, 1]),
     (4096, 11008, 4096, "gemm_f32_mfma_256x256x32_tail128", [512, 1, 1]),  # 688 tiles: 2 rounds + 176 as 128x128
     (3072, 3072, 3072, "gemm_f32_mfma_64x64x32", [2304, 1, 1]),  # 128x128 would fill 56% of two rounds
     (2500, 2500, 2500, "gemm_f32_mfma_128x128x32", [400, 1, 1]),
@@ -173,15 +177,17 @@ def test_constant_bits_round_trip():
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
     # 256x256 for the whole rounds of a grid of >= 256 such tiles (the rest as
-    # 128x128); else the best of 128x128 / 128x64 / 64x64 by round fill x tile
-    # efficiency among grids of >= 384 workgroups; K split only below half the CUs.
+    # 128x128); direct-load 32x32 tiles for aligned small grids with moderate K;
+    # else the best of 128x128 / 128x64 / 64x64 by round fill x tile efficiency
+    # among grids of >= 384 workgroups; K split only below half the CUs.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
     assert launch["kernel"] == kernel and launch["grid"] == grid, launch
 
 
 def test_descriptions_report_workspace_bytes():
     # Split launches own a workspace allocated at jr_compile; others none.
-    assert describe({"op": "gemm", "m": 512, "n": 512, "k": 512, "tiled": True})["workspace_bytes"] == 4 * 512 * 512 * 4
+    assert describe({"op": "gemm", "m": 256, "n": 256, "k": 4096, "tiled": True})["workspace_bytes"] == 16 * 256 * 256 * 4
+    assert describe({"op": "gemm", "m": 512, "n": 512, "k": 512, "tiled": True})["workspace_bytes"] == 0
     assert describe({"op": "gemm", "m": 4096, "n": 4096, "k": 4096, "tiled": True})["workspace_bytes"] == 0
     assert describe({"op": "attention_online", "heads": 8, "seq": 1024, "dim": 64, "causal": True})["workspace_bytes"] > 0
     assert describe({"op": "attention_online", "heads": 128, "seq": 4096, "dim": 128, "causal": True})[
