@@ -100,9 +100,9 @@ __device__ inline int swz_b(int row) { return row & 7; }
 
 template <int TM, int TN>
 __device__ inline void issue_stage_dma(const float *__restrict__ A, const float *__restrict__ B, int N, int K,
-                                       int m0, int n0, int k0, uint32_t stage_lds) {
+                                       int m0, int n0, int k0, uint32_t stage_lds, int t) {
     using T = Tile<TM, TN>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = t & 63, wave = t >> 6;
     const float *abase = A + size_t(m0) * K + k0;
     const float *bbase = B + size_t(k0) * N + n0;
     const uint32_t sb = stage_lds + T::kAStageS * 4;
@@ -151,9 +151,8 @@ __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
 template <int TM, int TN, bool VEC, bool GUARD>
 __device__ inline void load_stage(const float *__restrict__ A, const float *__restrict__ B, int M, int N, int K,
                                   int kend, int m0, int n0, int k0, f32x4 (&ra)[Tile<TM, TN>::kALoads],
-                                  f32x4 (&rb)[Tile<TM, TN>::kBLoads]) {
+                                  f32x4 (&rb)[Tile<TM, TN>::kBLoads], int t) {
     using T = Tile<TM, TN>;
-    const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < T::kALoads; ++i) {
         const int f = t + i * kThreads;
@@ -193,9 +192,8 @@ __device__ inline void load_stage(const float *__restrict__ A, const float *__re
 
 template <int TM, int TN>
 __device__ inline void store_stage(float *stage, const f32x4 (&ra)[Tile<TM, TN>::kALoads],
-                                   const f32x4 (&rb)[Tile<TM, TN>::kBLoads]) {
+                                   const f32x4 (&rb)[Tile<TM, TN>::kBLoads], int t) {
     using T = Tile<TM, TN>;
-    const int t = threadIdx.x;
     float *as = stage, *bs = stage + T::kAStage;
 #pragma unroll
     for (int i = 0; i < T::kALoads; ++i) {
@@ -285,21 +283,23 @@ __device__ inline void mma_stage_swz(const float *stage, int wm, int wn, int lan
 // The K loop for interior tiles: LDS-direct loads of stage kt+1 run while the
 // matrix cores consume stage kt; each wave drains its own loads, then one
 // barrier publishes the stage and retires the buffer the next loads overwrite.
+// `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
+// group (every group of a workgroup runs the same number of stages, so the
+// barriers match).
 template <int TM, int TN>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
-                                  int K, int kbegin, int kend, int m0, int n0, int wm, int wn, int lane,
+                                  int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
                                   f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     const uint32_t lds0 = lds_address(smem);
-    const int nk = (kend - kbegin) / kBK;
-    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin, lds0);
+    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin, lds0, t);
     drain_vmem();
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const float *cur = smem + (kt & 1) * T::kStageS;
         if (kt + 1 < nk)
             issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin + (kt + 1) * kBK,
-                                    lds0 + uint32_t(((kt + 1) & 1) * T::kStageS * 4));
+                                    lds0 + uint32_t(((kt + 1) & 1) * T::kStageS * 4), t);
         // Raised wave priority while this wave has matrix work, so the SIMD's
         // arbiter favours it over the co-resident workgroup's loads and folds
         // (measured +1-2% at 4096^3).
@@ -318,28 +318,28 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
 
 // The K loop of one workgroup: prefetch stage kt+1 into registers while the
 // matrix cores consume stage kt from LDS, then publish it with one barrier.
+// `nk` stages from kbegin; loads at or past kend read zero.
 template <int TM, int TN, bool VEC, bool GUARD>
 __device__ inline void k_loop(const float *__restrict__ A, const float *__restrict__ B, float *smem, int M, int N,
-                              int K, int kbegin, int kend, int m0, int n0, int wm, int wn, int lane,
+                              int K, int kbegin, int kend, int nk, int m0, int n0, int wm, int wn, int lane, int t,
                               f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     f32x4 ra[T::kALoads], rb[T::kBLoads];
-    const int nk = (kend - kbegin + kBK - 1) / kBK;
-    load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb);
-    store_stage<TM, TN>(smem, ra, rb);
+    load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb, t);
+    store_stage<TM, TN>(smem, ra, rb, t);
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
         const float *cur = smem + (kt & 1) * T::kStage;
         float *nxt = smem + ((kt + 1) & 1) * T::kStage;
         const bool more = kt + 1 < nk;
-        if (more) load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb);
+        if (more) load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb, t);
         f32x16 part[TM][TN];
         mma_stage<TM, TN>(cur, wm, wn, lane, part);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-        if (more) store_stage<TM, TN>(nxt, ra, rb);
+        if (more) store_stage<TM, TN>(nxt, ra, rb, t);
         __syncthreads();
     }
 }
@@ -366,12 +366,22 @@ struct PairArgs {
     int tiles;
 };
 
-template <int TM, int TN, bool VEC, int PATH>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
+// KG > 1: KG groups of four waves share the workgroup's tile. Group g sums
+// the g-th run of ceil(stages / KG) stages of the workgroup's K range (every
+// group runs that many, so the barriers match; stages past the range read
+// zero), each group with its own double-buffered stages in LDS. Groups
+// 1..KG-1 then leave their sums in LDS and group 0 adds them in group order.
+// KG = 2 puts two waves on each SIMD where a grid of 64x64 tiles gives each
+// CU one workgroup, so one wave's barrier and LDS waits overlap the other's
+// matrix work. Not used with pair or tail launches.
+template <int TM, int TN, bool VEC, int PATH, int KG = 1>
+__global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
     int tiles_m, int tiles_n, int kchunk, int tail_base, PairArgs pair) {
     using T = Tile<TM, TN>;
-    __shared__ float smem[2 * T::kStage];
+    __shared__ float smem[KG * 2 * T::kStage];
+    static_assert(KG == 1 || (KG - 1) * kThreads * TM * TN * 16 <= KG * 2 * T::kStage,
+                  "group sums must fit in the stage buffers");
     int tm, tn;
     if (pair.tiles > 0) {
         int pos = xcd_order(int(blockIdx.x), int(gridDim.x));
@@ -392,10 +402,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         tile_coords(tiles_m, tiles_n, tm, tn);
     }
     const int m0 = tm * T::kBM, n0 = tn * T::kBN;
-    const int kbegin = int(blockIdx.y) * kchunk;
-    const int kend = min(K, kbegin + kchunk);
+    const int kfirst = int(blockIdx.y) * kchunk;
+    const int klast = min(K, kfirst + kchunk);
+    const int group = KG > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kThreads) : 0;
+    const int t = int(threadIdx.x) % kThreads;
+    const int nk = ((klast - kfirst + kBK - 1) / kBK + KG - 1) / KG;  // stages per group
+    const int kbegin = kfirst + group * nk * kBK;
+    const int kend = min(klast, kbegin + nk * kBK);
+    float *gsmem = smem + group * 2 * T::kStage;
     float *__restrict__ out = C + size_t(blockIdx.y) * size_t(M) * size_t(N);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
     f32x16 acc[TM][TN];
@@ -407,12 +423,37 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
     // Interior tiles with 16-byte rows stream through LDS-direct loads; edge
-    // tiles and unaligned shapes take the guarded, register-staged path.
-    const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && (kend - kbegin) % kBK == 0;
+    // tiles, unaligned shapes and K ranges that are not KG x nk whole stages
+    // take the guarded, register-staged path.
+    const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && klast - kfirst == KG * nk * kBK;
     if (PATH == kDmaOnly || (VEC && interior))
-        k_loop_dma<TM, TN>(A, B, smem, N, K, kbegin, kend, m0, n0, wm, wn, lane, acc);
+        k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     else
-        k_loop<TM, TN, VEC, true>(A, B, smem, M, N, K, kbegin, kend, m0, n0, wm, wn, lane, acc);
+        k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
+
+    if (KG > 1) {  // both loops end on a barrier: the stage buffers are free
+        if (group > 0) {
+            float *dst = smem + (group - 1) * TM * TN * 16 * kThreads;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) dst[((i * TN + j) * 16 + v) * kThreads + t] = acc[i][j][v];
+        }
+        __syncthreads();
+        if (group > 0) return;
+#pragma unroll
+        for (int w = 1; w < KG; ++w) {
+            const float *src = smem + (w - 1) * TM * TN * 16 * kThreads;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) acc[i][j][v] += src[((i * TN + j) * 16 + v) * kThreads + t];
+        }
+    }
 
     const int h = lane >> 5, c = lane & 31;
 #pragma unroll
@@ -687,12 +728,13 @@ struct Plan {
     bool big;       // 256x256 eight-wave tile (tiles_m/tiles_n count 256x256 tiles)
     int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
     int direct;     // > 0: gemm_f32_direct with this many waves (tiles_m/tiles_n count 32x32 tiles)
+    int kgroups;    // 2: 64x64 tiles with two K groups of four waves (0 or 1: one group)
 };
 
 constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
 constexpr int kMinGroups = 384;    // a tile shape needs ~1.5 workgroups per CU to be considered
-constexpr int kSplitBelow = 128;   // 64x64 grids below half the CUs split K
-constexpr int kSplitTarget = 256;  // ... into about one workgroup per CU
+constexpr int kCUs = 256;
+constexpr int kSplitTarget = 256;  // split K into about one workgroup per CU
 constexpr int kMinChunk = 128;
 
 // Tile choice among 128x128, 128x64 and 64x64 (128x64 measured at or above
@@ -702,11 +744,17 @@ constexpr int kMinChunk = 128;
 // 1.00 / 0.97 / 0.90 its throughput on whole rounds. Measured on MI355X:
 // 3072^3 runs 64x64 at 111 TFLOP/s (128x128, whose second round is 12% full:
 // 94); 6144x1024x1024 64x64 109 (128x64: 93); 2500^3 128x128 88 (128x64: 82);
-// 1024x4096x4096 128x64 124 (64x128: 117). Below that, 64x64; K is split only
-// when the 64x64 grid covers fewer than half the CUs: 1024^3 ran at 83 TFLOP/s
-// unsplit and 74 split in two, 512^3 at 28 split in four and 20 unsplit.
-
-constexpr int kCUs = 256;
+// 1024x4096x4096 128x64 124 (64x128: 117).
+//
+// Below kMinGroups, 64x64 tiles, chosen by the tile count t:
+//  * 256 < t < 384: one K group (1536x1024x1024 40.4 us; two groups 43.7).
+//  * 128 < t <= 256: one workgroup per CU with two K groups, so two waves
+//    share each SIMD: 1024^3 25.7 -> 22.8 us, 768^3 19.7 -> 17.6,
+//    1000x777x512 17.2 -> 14.6, 1024x1024x4096 94.5 -> 81.6.
+//  * t <= 128: the direct-load 32x32 kernel when it applies (below), else K
+//    split over about kSplitTarget workgroups of two K groups each, then an
+//    ordered reduction: 1024x512x1024 25.2 us unsplit, 16.7 split in two;
+//    512x1024x2048 48.3 -> 25.8. A K group needs two stages or more.
 
 // The 256x256 tile runs one workgroup per CU, so it takes the whole rounds of
 // 256 tiles of a grid of 256x256 tiles; the rest of the grid (a partial round)
@@ -720,22 +768,22 @@ bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     return uint64_t(m / big::kBM) * (n / big::kBN) >= uint64_t(kCUs);
 }
 
-// Direct-load 32x32 tiles (one launch, K split over the waves of a workgroup)
-// for grids of fewer 64x64 tiles than CUs, aligned A rows, at least 64 tiles
-// of 32x32 and at most 16 slices of 32 k per wave: G = 4 waves up to 512 such
-// tiles, else 2, and no more waves than slices. Measured on MI355X against the
-// 64x64 / split-K plans: 512^3 7.4 against 9.6 us, 384^3 6.8 against 7.9,
-// 700^3 14.9 against 16.9, 1024x512x1024 18.1 against 25.4, 1000x777x512 17.7
-// against 21.9. With K = 8192 the split-K plan is 2-3x faster, and unaligned
-// rows (K = 513) cost the direct loads more than the LDS-staged kernel.
+// Direct-load 32x32 tiles (one launch, K split over the four waves of a
+// workgroup) for grids of at most 128 64x64 tiles, aligned A rows, at least
+// 64 tiles of 32x32 and at most 6 slices of 32 k per wave (no more waves than
+// slices). Measured on MI355X: 512^3 7.5 us against 9.6 split in four,
+// 384^3 6.8 against 7.9, 700^3 15.0 against 18.8 for 64x64 tiles with two K
+// groups. At 8 slices per wave the split plan wins (1024x512x1024 18.1
+// against 16.7), and unaligned rows (K = 513) cost the direct loads more than
+// the LDS-staged kernel.
 int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
     if (k % 4 != 0) return 0;
     const uint64_t t64 = uint64_t((m + 63) / 64) * ((n + 63) / 64);
     const uint64_t t32 = uint64_t((m + 31) / 32) * ((n + 31) / 32);
-    if (t64 >= uint64_t(kCUs) || t32 < 64) return 0;
+    if (t64 > uint64_t(kCUs / 2) || t32 < 64) return 0;
     const uint32_t slices = (k + kBK - 1) / kBK;
-    int g = t32 > 512 ? 2 : 4;
-    if (slices > uint32_t(16 * g)) return 0;
+    if (slices > 4 * 6) return 0;
+    int g = 4;
     while (g > 1 && uint32_t(g) > slices) g /= 2;
     return g;
 }
@@ -743,14 +791,12 @@ int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
-        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0};
+        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0, 1};
     }
     const int kchunk = int(((k + kBK - 1) / kBK) * kBK);
-    if (const int g = direct_waves(m, n, k))
-        return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g};
     auto grid = [&](int tm, int tn) {
         return Plan{tm, tn, 1, kchunk, int((m + 64 * tm - 1) / (64 * tm)), int((n + 64 * tn - 1) / (64 * tn)), false,
-                    0, 0};
+                    0, 0, 1};
     };
     const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
     const double eff[3] = {1.00, 0.97, 0.90};
@@ -767,7 +813,10 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (best >= 0) return grid(shapes[best][0], shapes[best][1]);
     Plan p = grid(1, 1);
     const int t = p.tiles_m * p.tiles_n;
-    if (t < kSplitBelow) {
+    if (t > kCUs) return p;
+    if (t <= kCUs / 2) {
+        if (const int g = direct_waves(m, n, k))
+            return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1};
         const int want = (kSplitTarget + t - 1) / t;
         const int most = int(k / kMinChunk);
         p.slices = std::max(1, std::min(want, most));
@@ -777,25 +826,28 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
             p.slices = int((k + p.kchunk - 1) / p.kchunk);
         }
     }
+    if (p.kchunk >= 2 * kBK) p.kgroups = 2;
     return p;
 }
 
-template <int TM, int TN>
+template <int TM, int TN, int KG = 1>
 void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
                  uint32_t m, uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
     const unsigned groups = unsigned(p.tiles_m) * unsigned(p.tiles_n) * (pair.tiles > 0 ? 2u : 1u);
-    const dim3 grid(groups, unsigned(p.slices)), block(kThreads);
-    const bool all_interior = vec && m % (64 * TM) == 0 && n % (64 * TN) == 0 && p.kchunk % kBK == 0 &&
-                              k % uint32_t(p.kchunk) % kBK == 0;
+    const dim3 grid(groups, unsigned(p.slices)), block(kThreads * KG);
+    // Every K slice (the last may be shorter) must be a multiple of KG whole stages.
+    const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
+    const bool all_interior = vec && m % (64 * TM) == 0 && n % (64 * TN) == 0 && chunk % (kBK * KG) == 0 &&
+                              last % (kBK * KG) == 0;
     if (all_interior)
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly>), grid, block, 0, stream, a, b, out, int(m),
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
                            int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
     else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out, int(m),
+                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                           int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out, int(m),
+                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
 }
 
 }  // namespace
@@ -820,7 +872,13 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                 {uint32_t(64 * p.direct), 1, 1},
                 uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
     }
-    // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 grids split K.
+    // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
+    // run two K groups.
+    if (p.kgroups == 2)
+        return {p.slices > 1 ? "gemm_f32_mfma_64x64x32_splitk_k2" : "gemm_f32_mfma_64x64x32_k2",
+                {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
+                {2 * kThreads, 1, 1},
+                2 * Tile<1, 1>::kLdsBytes};
     const int shape = p.tm == 2 ? (p.tn == 2 ? 2 : 1) : 0;
     static const char *names[3][2] = {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
                                       {"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},
@@ -835,13 +893,13 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
 
 bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    return !p.big && !p.direct && p.slices == 1 && m > 0 && n > 0 && k > 0;
+    return !p.big && !p.direct && p.kgroups != 2 && p.slices == 1 && m > 0 && n > 0 && k > 0;
 }
 
 hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
                          const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    if (p.big || p.direct || p.slices != 1) return hipErrorInvalidValue;
+    if (p.big || p.direct || p.kgroups == 2 || p.slices != 1) return hipErrorInvalidValue;
     const uintptr_t bits = reinterpret_cast<uintptr_t>(a0) | reinterpret_cast<uintptr_t>(b0) |
                            reinterpret_cast<uintptr_t>(a1) | reinterpret_cast<uintptr_t>(b1);
     const bool vec = (bits & 15u) == 0 && (k % 4 == 0) && (n % 4 == 0);
@@ -871,7 +929,7 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         }
         // Unaligned pointers: the 128x128 register-staged path (no split: the
         // grid is large).
-        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0};
+        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0, 1};
         launch_tile<2, 2>(stream, q, false, a, b, c, m, n, k);
         return hipGetLastError();
     }
@@ -879,7 +937,7 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
         if ((reinterpret_cast<uintptr_t>(a) & 15u) != 0) {
             // Unaligned A: the 64x64 register-staged tiles (no split, no workspace).
-            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0};
+            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0, 1};
             launch_tile<1, 1>(stream, q, false, a, b, c, m, n, k);
         } else if (p.direct == 4) {
             hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
@@ -894,7 +952,8 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         return hipGetLastError();
     }
     float *out = p.slices > 1 ? workspace : c;
-    if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
+    if (p.kgroups == 2) launch_tile<1, 1, 2>(stream, p, vec, a, b, out, m, n, k);
+    else if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);
     else launch_tile<1, 1>(stream, p, vec, a, b, out, m, n, k);
     hipError_t status = hipGetLastError();

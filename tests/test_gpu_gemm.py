@@ -112,8 +112,8 @@ def test_edge_masking_shapes(runtime, m, n, k):
     gate(got, m, n, k, a, b)
 
 
-@pytest.mark.parametrize("m,n,k,waves", [(300, 200, 100, 4), (1000, 777, 512, 2), (512, 512, 2048, 4),
-                                          (257, 255, 36, 2), (255, 257, 4, 1), (96, 700, 1020, 4),
+@pytest.mark.parametrize("m,n,k,waves", [(300, 200, 100, 4), (384, 320, 768, 4), (130, 520, 388, 4),
+                                          (257, 255, 36, 2), (64, 2048, 96, 2), (255, 257, 4, 1),
                                           (700, 700, 700, 4), (2047, 33, 164, 4)])
 def test_direct_tile_shapes(runtime, m, n, k, waves):
     # The direct-load 32x32 kernel: ragged M and N (clamped rows and columns that
@@ -124,6 +124,28 @@ def test_direct_tile_shapes(runtime, m, n, k, waves):
     assert kernel.launch["kernel"] == f"gemm_f32_direct_32x32x32_w{waves}", kernel.launch
     a = orc.values(m * k, 0x99, 1.0)
     b = orc.values(k * n, 0xAA, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    gate(got, m, n, k, a, b)
+
+
+@pytest.mark.parametrize("m,n,k,kernel", [
+    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 16 per group
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # register-staged (unaligned), last group partial
+    (768, 768, 768, "gemm_f32_mfma_64x64x32_k2"),
+    (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial
+    (65, 67, 63, "gemm_f32_mfma_64x64x32_k2"),  # one stage per group
+    (100, 100, 40, "gemm_f32_mfma_64x64x32_k2"),  # group 1's stage lies mostly past K
+    (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2"),
+    (200, 8, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),  # ragged last slice
+    (1, 1024, 4096, "gemm_f32_mfma_64x64x32_splitk_k2"),
+])
+def test_two_group_tile_shapes(runtime, m, n, k, kernel):
+    # 64x64 tiles whose two K groups of four waves sum the two halves of each
+    # workgroup's K range and meet in LDS.
+    launch = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch
+    assert launch["kernel"] == kernel, launch
+    a = orc.values(m * k, 0xBB, 1.0)
+    b = orc.values(k * n, 0xCC, 1.0)
     got = run_gemm(runtime, m, n, k, a, b, repeats=2)
     gate(got, m, n, k, a, b)
 
