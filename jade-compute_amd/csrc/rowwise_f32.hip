@@ -115,15 +115,17 @@ __global__ __launch_bounds__(kThreads) void softmax_cached(const float *__restri
     }
 }
 
-// Rows of 1024..16384 floats (cols % 4 == 0): one row per 256-thread block,
-// V float4 per lane, cross-wave reductions through LDS. Spreading a row over
-// four waves keeps each wave's burst at V KiB; a 16 KiB burst per wave (the
-// wave-per-row kernel at 4096 columns) capped the stream at ~5.5 TB/s, where
-// this layout with non-temporal loads and stores reached ~6.2 TB/s.
-template <int V>
-__global__ __launch_bounds__(kThreads) void softmax_block(const float *__restrict__ x, float *__restrict__ out,
-                                                          int cols) {
-    __shared__ float partial[2][kRowsPerBlock];
+// Rows of 1024..16384 floats (cols % 4 == 0): one row per block of T threads
+// (256 below 2048 columns, else 512), V float4 per lane, cross-wave
+// reductions through LDS. Spreading a row over several waves keeps each
+// wave's burst small: a 16 KiB burst per wave (the wave-per-row kernel at 4096
+// columns) capped the stream at ~5.5 TB/s. At 32768x4096 (1 GiB moved) 256
+// threads per row ran at 6.35 TB/s and 512 at 6.58, against 6.34 TB/s for a
+// plain non-temporal copy of the same 512 MiB; 1024 threads ran at 5.97.
+template <int T, int V>
+__global__ __launch_bounds__(T) void softmax_block(const float *__restrict__ x, float *__restrict__ out, int cols) {
+    constexpr int W = T / 64;
+    __shared__ float partial[2][W];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n4 = cols >> 2;
     const f32x4 *xr = reinterpret_cast<const f32x4 *>(x + size_t(blockIdx.x) * cols);
@@ -131,14 +133,16 @@ __global__ __launch_bounds__(kThreads) void softmax_block(const float *__restric
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-        const int idx = int(threadIdx.x) + kThreads * i;
+        const int idx = int(threadIdx.x) + T * i;
         v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
     }
     m = wave_max(m);
     if (lane == 0) partial[0][wave] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(partial[0][0], partial[0][1]), fmaxf(partial[0][2], partial[0][3]));
+    m = partial[0][0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) m = fmaxf(m, partial[0][w]);
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < V; ++i) {
@@ -151,11 +155,14 @@ __global__ __launch_bounds__(kThreads) void softmax_block(const float *__restric
     sum = wave_sum(sum);
     if (lane == 0) partial[1][wave] = sum;
     __syncthreads();
-    const float inv = 1.0f / ((partial[1][0] + partial[1][1]) + (partial[1][2] + partial[1][3]));
+    float total = partial[1][0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) total += partial[1][w];
+    const float inv = 1.0f / total;
     f32x4 *o4 = reinterpret_cast<f32x4 *>(out + size_t(blockIdx.x) * cols);
 #pragma unroll
     for (int i = 0; i < V; ++i) {
-        const int idx = int(threadIdx.x) + kThreads * i;
+        const int idx = int(threadIdx.x) + T * i;
         if (idx < n4) __builtin_nontemporal_store(v[i] * inv, o4 + idx);
     }
 }
@@ -195,12 +202,17 @@ int cache_slots(uint32_t cols) {
     return 0;
 }
 
-// float4 per lane of softmax_block for 1024 <= cols <= 16384, cols % 4 == 0;
-// 0 selects the wave-per-row kernels.
-int block_slots(uint32_t cols) {
+// softmax_block's threads per row for 1024 <= cols <= 16384, cols % 4 == 0
+// (0 selects the wave-per-row kernels), and its float4 per lane.
+int block_threads(uint32_t cols) {
     if (cols % 4 != 0 || cols < 1024 || cols > 16384) return 0;
-    const uint32_t per_lane = (cols / 4 + kThreads - 1) / kThreads;
-    return per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : per_lane <= 8 ? 8 : 16;
+    return cols < 2048 ? 256 : 512;
+}
+int block_slots(uint32_t cols) {
+    const int t = block_threads(cols);
+    if (!t) return 0;
+    const uint32_t per_lane = (cols / 4 + t - 1) / t;
+    return per_lane <= 1 ? 1 : per_lane <= 2 ? 2 : per_lane <= 4 ? 4 : 8;
 }
 
 bool aligned16(const void *a, const void *b, const void *c) {
@@ -232,8 +244,8 @@ hipError_t rms_norm_f32(hipStream_t stream, const float *x, const float *weight,
 }
 
 LaunchShape softmax_shape(uint32_t rows, uint32_t cols) {
-    const int blk = block_slots(cols);
-    if (blk) return {"softmax_block", {rows, 1, 1}, {kThreads, 1, 1}, 2 * kRowsPerBlock * sizeof(float)};
+    if (const int t = block_threads(cols))
+        return {"softmax_block", {rows, 1, 1}, {uint32_t(t), 1, 1}, uint32_t(2 * (t / 64) * sizeof(float))};
     const int c4 = cache_slots(cols);
     return {c4 ? "softmax_cached" : "softmax_rows", {(rows + kRowsPerBlock - 1) / kRowsPerBlock, 1, 1},
             {kThreads, 1, 1}, 0};
@@ -241,13 +253,22 @@ LaunchShape softmax_shape(uint32_t rows, uint32_t cols) {
 
 hipError_t softmax_f32(hipStream_t stream, const float *x, float *out, uint32_t rows, uint32_t cols) {
     const bool aligned = aligned16(x, out, out);
-    switch (aligned ? block_slots(cols) : 0) {
-        case 1: hipLaunchKernelGGL(softmax_block<1>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
-        case 2: hipLaunchKernelGGL(softmax_block<2>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
-        case 4: hipLaunchKernelGGL(softmax_block<4>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
-        case 8: hipLaunchKernelGGL(softmax_block<8>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
-        case 16: hipLaunchKernelGGL(softmax_block<16>, dim3(rows), dim3(kThreads), 0, stream, x, out, int(cols)); return hipGetLastError();
-        default: break;
+    const int bt = aligned ? block_threads(cols) : 0;
+    if (bt == 256) {
+        switch (block_slots(cols)) {
+            case 1: hipLaunchKernelGGL((softmax_block<256, 1>), dim3(rows), dim3(256), 0, stream, x, out, int(cols)); break;
+            default: hipLaunchKernelGGL((softmax_block<256, 2>), dim3(rows), dim3(256), 0, stream, x, out, int(cols)); break;
+        }
+        return hipGetLastError();
+    }
+    if (bt == 512) {
+        switch (block_slots(cols)) {
+            case 1: hipLaunchKernelGGL((softmax_block<512, 1>), dim3(rows), dim3(512), 0, stream, x, out, int(cols)); break;
+            case 2: hipLaunchKernelGGL((softmax_block<512, 2>), dim3(rows), dim3(512), 0, stream, x, out, int(cols)); break;
+            case 4: hipLaunchKernelGGL((softmax_block<512, 4>), dim3(rows), dim3(512), 0, stream, x, out, int(cols)); break;
+            default: hipLaunchKernelGGL((softmax_block<512, 8>), dim3(rows), dim3(512), 0, stream, x, out, int(cols)); break;
+        }
+        return hipGetLastError();
     }
     const dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(kThreads);
     const int c4 = aligned ? cache_slots(cols) : 0;

@@ -48,7 +48,8 @@ def test_softmax_config_32768x4096(runtime):
 
 
 @pytest.mark.parametrize("rows,cols", [(64, 4096), (3, 17), (2, 257), (5, 4100), (4, 6000), (1, 1), (33, 64),
-                                       (3, 1024), (2, 1020), (2, 2052), (2, 16384), (1, 16388)])
+                                       (3, 1024), (2, 1020), (2, 2052), (2, 16384), (1, 16388), (3, 1536),
+                                       (2, 2048), (2, 3000), (2, 8192), (2, 12000)])
 def test_softmax_shapes(runtime, rows, cols):
     x = orc.normal(rows * cols, 0x4321, 0.0, 2.0)
     got = run(runtime, {"op": "softmax", "rows": rows, "cols": cols}, [x], rows * cols)
@@ -108,9 +109,12 @@ def test_expression_interpreter_eight_inputs(runtime):
     assert_close(got, np.exp(-(acc * 0.125)), 3e-5)
 
 
-@pytest.mark.parametrize("cols,kernel", [(1020, "softmax_cached"), (1024, "softmax_block"), (4096, "softmax_block"),
-                                         (16384, "softmax_block"), (16388, "softmax_rows"), (1025, "softmax_rows")])
-def test_softmax_kernel_choice(runtime, cols, kernel):
-    # Rows of 1024..16384 floats take one block per row; others one wave per row.
+@pytest.mark.parametrize("cols,kernel,threads", [(1020, "softmax_cached", 256), (1024, "softmax_block", 256),
+                                                 (2048, "softmax_block", 512), (4096, "softmax_block", 512),
+                                                 (16384, "softmax_block", 512), (16388, "softmax_rows", 256),
+                                                 (1025, "softmax_rows", 256)])
+def test_softmax_kernel_choice(runtime, cols, kernel, threads):
+    # Rows of 1024..16384 floats take one block per row (512 threads from 2048
+    # columns); others one wave per row.
     launch = runtime.compile({"op": "softmax", "rows": 8, "cols": cols}).launch
-    assert launch["kernel"] == kernel, launch
+    assert launch["kernel"] == kernel and launch["block"][0] == threads, launch
