@@ -272,8 +272,12 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
             tile_sum = halves_sum(tile_sum);
             row_sum = row_sum * old_weight + tile_sum;
             row_max = next_max;
+            // Once the running maxima settle, old_weight is exactly 1 in every
+            // lane and the rescale is the identity: skip it (wave-uniform).
+            if (__any(old_weight != 1.0f)) {
 #pragma unroll
-            for (int b = 0; b < DP / 32; ++b) acc[b] *= old_weight;
+                for (int b = 0; b < DP / 32; ++b) acc[b] *= old_weight;
+            }
 
             // O^T += V^T P^T over the live sub-tiles.
 #pragma unroll
