@@ -344,6 +344,104 @@ __device__ inline void k_loop(const float *__restrict__ A, const float *__restri
     }
 }
 
+// ---- Unaligned shapes: two stages of register prefetch ----------------------
+// Rows that are not 16-byte aligned (K or N not a multiple of 4) load one
+// float at a time. With one stage in flight those loads bound the K loop
+// (~2.4 us per stage at 1000x777x513 against 0.43 us of matrix work), so the
+// unaligned loop keeps two stages in registers. The waits stay exact only if
+// the loads are branch-free: indices are clamped into A and B and every load
+// is issued; the k >= kend mask is applied when the stage is written to LDS,
+// one iteration after its loads. Clamped rows of A (columns of B) reach only
+// rows (columns) of the tile that are never stored, so they are not masked.
+template <int TM, int TN>
+struct Regs {
+    // One stage: a[j] = A[m0 + (t + 256j) / 32][k0 + (t + 256j) % 32] and
+    // b[j] = B[k0 + (t + 256j) / BN][n0 + (t + 256j) % BN]: consecutive lanes
+    // read consecutive floats of a row, so each load instruction covers two
+    // 128-byte rows of A or one 256-byte (BN = 64) row of B.
+    float a[Tile<TM, TN>::kBM * kBK / kThreads], b[kBK * Tile<TM, TN>::kBN / kThreads];
+};
+
+template <int TM, int TN>
+__device__ inline void load_stage_clamped(const float *__restrict__ A, const float *__restrict__ B, int M, int N,
+                                          int K, int m0, int n0, int k0, Regs<TM, TN> &r, int t) {
+    using T = Tile<TM, TN>;
+#pragma unroll
+    for (int j = 0; j < T::kBM * kBK / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        r.a[j] = A[size_t(min(m0 + f / kBK, M - 1)) * K + min(k0 + f % kBK, K - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < kBK * T::kBN / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        r.b[j] = B[size_t(min(k0 + f / T::kBN, K - 1)) * N + min(n0 + f % T::kBN, N - 1)];
+    }
+}
+
+// Writes a stage loaded by load_stage_clamped, zeroing k >= kend in A and B.
+template <int TM, int TN>
+__device__ inline void store_stage_masked(float *stage, const Regs<TM, TN> &r, int k0, int kend, int t) {
+    using T = Tile<TM, TN>;
+    float *as = stage, *bs = stage + T::kAStage;
+#pragma unroll
+    for (int j = 0; j < T::kBM * kBK / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        as[(f / kBK) * kLDA + f % kBK] = k0 + f % kBK < kend ? r.a[j] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kBK * T::kBN / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        bs[(f / T::kBN) * T::kLDB + f % T::kBN] = k0 + f / T::kBN < kend ? r.b[j] : 0.f;
+    }
+}
+
+// A barrier that orders LDS only: this wave's LDS reads and writes complete
+// before it, global loads stay in flight across it. __syncthreads() carries a
+// workgroup release fence, for which the compiler also waits for every
+// outstanding global load, which would drain the register prefetch each stage.
+// The "memory" clobber keeps the compiler from moving memory accesses across.
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// `nk` stages from kbegin; stage kt+2's loads are issued while stage kt is
+// consumed and stage kt+1 (loaded an iteration earlier) is written to LDS.
+template <int TM, int TN>
+__device__ inline void k_loop_unaligned(const float *__restrict__ A, const float *__restrict__ B, float *smem,
+                                        int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
+                                        int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
+    using T = Tile<TM, TN>;
+    Regs<TM, TN> r[2];
+    load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin, r[0], t);
+    __builtin_amdgcn_sched_barrier(0);
+    load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + kBK, r[1], t);
+    __builtin_amdgcn_sched_barrier(0);
+    store_stage_masked<TM, TN>(smem, r[0], kbegin, kend, t);
+    lds_barrier();
+    // Unrolled by two so the register stage in use is a compile-time index.
+    for (int kt = 0; kt < nk; kt += 2) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int k = kt + u;
+            if (k < nk) {  // block-uniform
+                const float *cur = smem + u * T::kStage;
+                // Unconditional, so every path into the loop has the same
+                // loads in flight and the waits below stay exact; stages past
+                // nk load clamped, in-bounds data that is never stored.
+                load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + (k + 2) * kBK, r[u], t);
+                __builtin_amdgcn_sched_barrier(0);
+                f32x16 part[TM][TN];
+                mma_stage<TM, TN>(cur, wm, wn, lane, part);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+                if (k + 1 < nk)
+                    store_stage_masked<TM, TN>(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK, kend, t);
+                lds_barrier();
+            }
+        }
+    }
+}
+
 // Two waves per SIMD (LDS allows two workgroups per CU at the largest tile);
 // the register budget is capped to match so stage and running accumulators fit.
 // gridDim.y > 1 splits K into slices of `kchunk` (a multiple of 32); slice z
@@ -428,6 +526,8 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && klast - kfirst == KG * nk * kBK;
     if (PATH == kDmaOnly || (VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
+    else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
+        k_loop_unaligned<TM, TN>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
