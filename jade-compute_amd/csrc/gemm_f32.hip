@@ -737,13 +737,19 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 }
 }  // namespace direct
 
+// gridDim.y > 1: a batch of independent products, product z at A + z*sa,
+// B + z*sb, C + z*sc (attention's P.V per head).
 template <int G>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
                                                           float *__restrict__ C, int M, int N, int K, int tiles_m,
-                                                          int tiles_n) {
+                                                          int tiles_n, size_t sa = 0, size_t sb = 0,
+                                                          size_t sc = 0) {
     using namespace direct;
     constexpr int D = kDepth;
     __shared__ float red[(G > 1 ? G - 1 : 1) * 16 * 64];
+    A += blockIdx.y * sa;
+    B += blockIdx.y * sb;
+    C += blockIdx.y * sc;
     int tm, tn;
     tile_coords(tiles_m, tiles_n, tm, tn);
     const int lane = threadIdx.x & 63;
@@ -1007,6 +1013,16 @@ hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, f
     if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else launch_tile<1, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    return hipGetLastError();
+}
+
+hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m,
+                                   uint32_t n, uint32_t k, uint32_t batch, size_t sa, size_t sb, size_t sc) {
+    if (k % 4 != 0 || ((reinterpret_cast<uintptr_t>(a) | sa * sizeof(float)) & 15u) != 0) return hipErrorInvalidValue;
+    const int tiles_m = int((m + 31) / 32), tiles_n = int((n + 31) / 32);
+    const dim3 grid(unsigned(tiles_m * tiles_n), batch), block(256);
+    hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), tiles_m, tiles_n, sa,
+                       sb, sc);
     return hipGetLastError();
 }
 

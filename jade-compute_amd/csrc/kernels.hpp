@@ -26,6 +26,12 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k);
 size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k);
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
                     uint32_t k, float *workspace);
+// `batch` independent products of one shape, product z at a + z*sa, b + z*sb,
+// c + z*sc (elements), on direct-load 32x32 tiles with four waves splitting K.
+// Needs k % 4 == 0 and 16-byte aligned rows of a (a and sa). For attention's
+// materialised P.V per head.
+hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m,
+                                   uint32_t n, uint32_t k, uint32_t batch, size_t sa, size_t sb, size_t sc);
 // Two independent products of one shape (c0 = a0 b0, c1 = a1 b1) in one
 // launch, for shapes whose plan needs no workspace and no 256x256 tile
 // (gemm_f32_pairable); each output is bit-identical to its own gemm_f32.

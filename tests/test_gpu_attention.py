@@ -61,6 +61,25 @@ def test_lab_attention_configs(runtime, h, s, d, causal, amp, zeros):
         assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
 
 
+@pytest.mark.parametrize("h,s,d,causal", [(2, 64, 64, True), (1, 512, 64, False), (3, 100, 36, True),
+                                          (2, 132, 128, True), (1, 8, 4, False), (4, 256, 20, False)])
+def test_materialised_on_matrix_cores(runtime, h, s, d, causal):
+    # Scores (dim % 4 == 0) and P.V (seq % 4 == 0) on the MFMA kernels: a
+    # partial last dim slice (36, 20), ragged 32x32 score tiles (100, 132),
+    # causal tiles wholly above the diagonal, and a dim below one slice (4).
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x1212), orc.normal(n, 0x3434), orc.normal(n, 0x5656)
+    for op in ("attention_scores", "attention_apply"):
+        spec = {"op": op, "heads": h, "seq": s, "dim": d}
+        if op == "attention_scores":
+            spec["causal"] = causal
+        assert runtime.compile(spec).launch["kernel"].endswith("_mfma")
+    got = run_materialised(runtime, h, s, d, causal, q, k, v)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
 def test_oracle_kat_on_device(runtime):
     q = np.zeros(6, np.float32)
     v = np.array([1, 2, 3, 4, 8, 9], np.float32)

@@ -197,3 +197,16 @@ def test_descriptions_report_workspace_bytes():
     assert describe({"op": "attention_online", "heads": 128, "seq": 4096, "dim": 128, "causal": True})[
         "workspace_bytes"] == 0
     assert describe({"op": "softmax", "rows": 4, "cols": 4})["workspace_bytes"] == 0
+
+
+@pytest.mark.parametrize("op,dim,seq,kernel", [
+    ("attention_scores", 64, 512, "attention_scores_mfma"), ("attention_scores", 5, 512, "attention_scores"),
+    ("attention_apply", 64, 512, "attention_apply_mfma"), ("attention_apply", 64, 513, "attention_apply"),
+])
+def test_materialised_attention_kernels(op, dim, seq, kernel):
+    # Scores run on the matrix cores when dim % 4 == 0, P.V when seq % 4 == 0
+    # (16-byte rows); other shapes take the one-thread-per-output kernels.
+    spec = {"op": op, "heads": 2, "seq": seq, "dim": dim}
+    if op == "attention_scores":
+        spec["causal"] = True
+    assert describe(spec)["launch"]["kernel"] == kernel
