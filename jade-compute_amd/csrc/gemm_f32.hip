@@ -10,10 +10,13 @@
 //  * Otherwise a 256-thread workgroup is a 2x2 grid of waves; each wave owns
 //    TM x TN blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per
 //    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64 or
-//    64x64. Two independent products of one shape can share a launch.
+//    64x64. Two independent products of one shape can share a launch. Grids
+//    of at most one 64x64 tile per CU run two such groups of four waves per
+//    workgroup (KG = 2), each over half of the tile's K stages.
 //  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
 //    LDS-direct loads (interior tiles) or a register prefetch (edge tiles and
-//    unaligned shapes), with one barrier per stage.
+//    unaligned shapes; unaligned 64x64 and 128x64 tiles keep two stages in
+//    registers), with one barrier per stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
