@@ -37,6 +37,7 @@
 //    gridDim.y: each slice writes a partial product to a workspace and a
 //    reduction kernel sums the slices in slice order (deterministic, no atomics).
 #include "kernels.hpp"
+#include "ops.hpp"
 
 #include <algorithm>
 
@@ -246,9 +247,10 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
     }
 }
 
-// mma_stage over the swizzled layout.
+// mma_stage over the swizzled layout: A stage at `as`, B stage at `bs`.
 template <int TM, int TN>
-__device__ inline void mma_stage_swz(const float *stage, int wm, int wn, int lane, f32x16 (&acc)[TM][TN]) {
+__device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, int wn, int lane,
+                                     f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
 #pragma unroll
@@ -263,7 +265,7 @@ __device__ inline void mma_stage_swz(const float *stage, int wm, int wn, int lan
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
             const int row = wm * 32 * TM + i * 32 + c, chunk = 4 * h + q;
-            a[i] = *reinterpret_cast<const f32x4 *>(stage + row * kBK + ((chunk ^ swz_a(row)) << 2));
+            a[i] = *reinterpret_cast<const f32x4 *>(as + row * kBK + ((chunk ^ swz_a(row)) << 2));
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -272,7 +274,7 @@ __device__ inline void mma_stage_swz(const float *stage, int wm, int wn, int lan
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int col = wn * 32 * TN + j * 32 + c;
-                b[j] = stage[T::kAStageS + krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
+                b[j] = bs[krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -308,7 +310,7 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
         // (measured +1-2% at 4096^3).
         __builtin_amdgcn_s_setprio(1);
         f32x16 part[TM][TN];
-        mma_stage_swz<TM, TN>(cur, wm, wn, lane, part);
+        mma_stage_swz<TM, TN>(cur, cur + T::kAStageS, wm, wn, lane, part);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -571,6 +573,111 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2
             }
         }
     }
+}
+
+// ---- Gate/up pair with a fused SwiGLU ---------------------------------------
+// G = A Bg, U = A Bu and Act = swiglu(G, U) for the residual MLP's gate and up
+// projections (src/runtime/workloads.rs:422-465), in one launch over 128x64
+// tiles: waves 0-3 compute the gate tile and waves 4-7 the up tile of the same
+// (row, column) block, from one LDS copy of the A stage and one B stage each.
+// Each output takes exactly the MFMA steps and folds of the 128x64 kernel, and
+// SwiGLU is the stream kernel's function, so all three outputs are
+// bit-identical to the two GEMM launches followed by the SwiGLU launch. The
+// up waves store U and pass it to the gate waves through LDS; the gate waves
+// store G and Act. Interior tiles only: M % 128 == 0, N % 64 == 0,
+// K % 32 == 0, 16-byte aligned rows.
+namespace dual {
+using T = Tile<2, 1>;
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kStage = T::kAStageS + 2 * T::kBStageS;  // A, then B for G, then B for U
+constexpr int kAInst = T::kAStageS * 4 / 1024 / kWaves, kBInst = T::kBStageS * 4 / 1024 / (kWaves / 2);
+static_assert(kAInst * kWaves * 1024 == T::kAStageS * 4 && kBInst * (kWaves / 2) * 1024 == T::kBStageS * 4,
+              "stage loads must split evenly over the waves");
+
+// Waves 0-3 load B for G, waves 4-7 B for U; all eight load A.
+__device__ inline void issue_stage(const float *__restrict__ A, const float *__restrict__ B, int N, int K, int m0,
+                                   int n0, int k0, uint32_t stage_lds, int wave, int lane) {
+    const float *abase = A + size_t(m0) * K + k0;
+#pragma unroll
+    for (int i = 0; i < kAInst; ++i) {  // eight 128-byte A rows per 1 KiB load
+        const int inst = wave * kAInst + i;
+        const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
+        lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
+    }
+    const float *bbase = B + size_t(k0) * N + n0;
+    const uint32_t sb = stage_lds + (T::kAStageS + (wave >> 2) * T::kBStageS) * 4;
+    constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
+#pragma unroll
+    for (int i = 0; i < kBInst; ++i) {  // four 256-byte B rows per 1 KiB load
+        const int inst = (wave & 3) * kBInst + i;
+        const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
+        lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
+    }
+}
+}  // namespace dual
+
+__global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
+    const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu, float *__restrict__ G,
+    float *__restrict__ U, float *__restrict__ Act, int N, int K, int tiles_m, int tiles_n) {
+    using namespace dual;
+    __shared__ float smem[2 * kStage];
+    int tm, tn;
+    tile_coords(tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * T::kBM, n0 = tn * T::kBN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int group = wave >> 2, wl = wave & 3;  // group 0: G, group 1: U
+    const int wm = wl >> 1, wn = wl & 1;
+    const float *B = group ? Bu : Bg;
+    const uint32_t lds0 = lds_address(smem);
+    f32x16 acc[2][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][0][v] = 0.f;
+    const int nk = K / kBK;
+    dual::issue_stage(A, B, N, K, m0, n0, 0, lds0, wave, lane);
+    drain_vmem();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const float *cur = smem + (kt & 1) * kStage;
+        if (kt + 1 < nk)
+            dual::issue_stage(A, B, N, K, m0, n0, (kt + 1) * kBK, lds0 + uint32_t(((kt + 1) & 1) * kStage * 4), wave,
+                              lane);
+        __builtin_amdgcn_s_setprio(1);
+        f32x16 part[2][1];
+        mma_stage_swz<2, 1>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) acc[i][0] += part[i][0];
+        __builtin_amdgcn_s_setprio(0);
+        drain_vmem();
+        __syncthreads();
+    }
+    // The loop ended on a barrier: the stage buffers are free for U.
+    const int h = lane >> 5, c = lane & 31;
+    const int col = n0 + wn * 32 + c;
+    float *ushare = smem;  // [i][v][256 threads of the U group]
+    if (group == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                U[size_t(row) * N + col] = acc[i][0][v];
+                ushare[(i * 16 + v) * 256 + wl * 64 + lane] = acc[i][0][v];
+            }
+    }
+    __syncthreads();
+    if (group == 1) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            const float g = acc[i][0][v], u = ushare[(i * 16 + v) * 256 + wl * 64 + lane];
+            G[size_t(row) * N + col] = g;
+            Act[size_t(row) * N + col] = swiglu(g, u);
+        }
 }
 
 // ---- 256x256 tile, eight waves of 128x64 ---------------------------------
@@ -1016,6 +1123,25 @@ hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, f
     if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
     else launch_tile<1, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
+    return hipGetLastError();
+}
+
+bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
+    // The plan the pair would take must be the 128x64 tile, so the fused
+    // outputs are the pair's bits.
+    const Plan p = plan_for(m, n, k);
+    return !p.big && !p.direct && p.kgroups != 2 && p.slices == 1 && p.tm == 2 && p.tn == 1 &&
+           m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 && k > 0;
+}
+
+hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,
+                                float *u, float *act, uint32_t m, uint32_t n, uint32_t k) {
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(bg) |
+                           reinterpret_cast<uintptr_t>(bu);
+    if (!gemm_f32_dual_swiglu_fits(m, n, k) || (bits & 15u) != 0) return hipErrorInvalidValue;
+    const int tiles_m = int(m / dual::T::kBM), tiles_n = int(n / dual::T::kBN);
+    hipLaunchKernelGGL(gemm_f32_dual_swiglu, dim3(unsigned(tiles_m * tiles_n)), dim3(dual::kThreads), 0, stream, a, bg,
+                       bu, g, u, act, int(n), int(k), tiles_m, tiles_n);
     return hipGetLastError();
 }
 

@@ -32,6 +32,14 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
 // materialised P.V per head.
 hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m,
                                    uint32_t n, uint32_t k, uint32_t batch, size_t sa, size_t sb, size_t sc);
+// The residual MLP's gate/up pair with SwiGLU fused: g = a bg, u = a bu and
+// act = swiglu(g, u) in one launch, each output bit-identical to the paired
+// GEMM launch followed by swiglu_f32. Only where gemm_f32_dual_swiglu_fits
+// (shapes whose plan is whole 128x64 tiles) and a, bg, bu are 16-byte
+// aligned; otherwise returns hipErrorInvalidValue without launching.
+bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k);
+hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,
+                                float *u, float *act, uint32_t m, uint32_t n, uint32_t k);
 // Two independent products of one shape (c0 = a0 b0, c1 = a1 b1) in one
 // launch, for shapes whose plan needs no workspace and no 256x256 tile
 // (gemm_f32_pairable); each output is bit-identical to its own gemm_f32.

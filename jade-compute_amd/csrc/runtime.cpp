@@ -565,6 +565,25 @@ static bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
     return true;
 }
 
+// Three consecutive jobs run as one fused launch when they are the residual
+// MLP's gate and up projections and their SwiGLU (src/runtime/workloads.rs:
+// 440-465): two pairable GEMMs on the same A, then swi_glu(x's C, y's C -> D)
+// over m*n elements, with D none of the GEMMs' inputs, a shape whose plan is
+// whole 128x64 tiles and 16-byte aligned inputs. The three outputs are
+// bit-identical to the ordered launches (gemm_f32_dual_swiglu).
+static bool fusable_gate_up_swiglu(const jr_dispatch &x, const jr_dispatch &y, const jr_dispatch &z) {
+    if (!pairable(x, y) || z.buffer_count != 3) return false;
+    const KernelSpec &g = static_cast<Pipeline *>(x.kernel)->spec;
+    const KernelSpec &f = static_cast<Pipeline *>(z.kernel)->spec;
+    if (f.op != Op::SwiGlu || uint64_t(f.len) != uint64_t(g.m) * g.n) return false;
+    if (x.buffers[0] != y.buffers[0] || z.buffers[0] != x.buffers[2] || z.buffers[1] != y.buffers[2]) return false;
+    void *const d = z.buffers[2];
+    if (d == x.buffers[0] || d == x.buffers[1] || d == y.buffers[1]) return false;
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(x.buffers[0]) | reinterpret_cast<uintptr_t>(x.buffers[1]) |
+                           reinterpret_cast<uintptr_t>(y.buffers[1]);
+    return (bits & 15u) == 0 && jade::hipk::gemm_f32_dual_swiglu_fits(g.m, g.n, g.k);
+}
+
 extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size_t job_count, uint32_t repeats,
                                      double *gpu_ms, char *err, size_t cap) {
     clear(err, cap);
@@ -597,16 +616,34 @@ extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size
     }
     const int rc = select(ctx, err, cap);
     if (rc) return rc;
-    // Adjacent independent GEMMs of one shape share a launch (pairable()).
-    std::vector<bool> paired(job_count, false);
-    for (size_t j = 0; j + 1 < job_count; ++j)
-        if (!paired[j] && pairable(jobs[j], jobs[j + 1])) paired[j] = true, ++j;
+    // The MLP's gate/up GEMMs and SwiGLU fuse into one launch
+    // (fusable_gate_up_swiglu()); other adjacent independent GEMMs of one
+    // shape share a launch (pairable()).
+    std::vector<bool> paired(job_count, false), fused(job_count, false);
+    for (size_t j = 0; j + 1 < job_count; ++j) {
+        if (j + 2 < job_count && fusable_gate_up_swiglu(jobs[j], jobs[j + 1], jobs[j + 2])) {
+            fused[j] = true;
+            j += 2;
+        } else if (pairable(jobs[j], jobs[j + 1])) {
+            paired[j] = true;
+            ++j;
+        }
+    }
     return timed_sequence(
         ctx, repeats, gpu_ms,
         [&]() -> hipError_t {
             for (size_t j = 0; j < job_count; ++j) {
                 hipError_t status;
-                if (paired[j]) {
+                if (fused[j]) {
+                    const KernelSpec &s = static_cast<Pipeline *>(jobs[j].kernel)->spec;
+                    void *const *x = jobs[j].buffers;
+                    void *const *y = jobs[j + 1].buffers;
+                    status = jade::hipk::gemm_f32_dual_swiglu(
+                        ctx->stream, static_cast<const float *>(x[0]), static_cast<const float *>(x[1]),
+                        static_cast<const float *>(y[1]), static_cast<float *>(x[2]), static_cast<float *>(y[2]),
+                        static_cast<float *>(jobs[j + 2].buffers[2]), s.m, s.n, s.k);
+                    j += 2;
+                } else if (paired[j]) {
                     const KernelSpec &s = static_cast<Pipeline *>(jobs[j].kernel)->spec;
                     void *const *x = jobs[j].buffers;
                     void *const *y = jobs[j + 1].buffers;

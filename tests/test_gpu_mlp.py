@@ -59,3 +59,59 @@ def test_config_c4_mlp(runtime):
                    float(np.float32(eps)))
     check = orc.compare(got[rows].reshape(-1), want, 1e-4, 1e-4)
     assert check.status == 0, check.first_bad
+
+
+def _run_jobs(runtime, specs, arrays, plan, repeats=1, one_at_a_time=False):
+    # specs: name -> spec; arrays: name -> host array or element count;
+    # plan: list of (spec name, [buffer names]).
+    kernels = {name: runtime.compile(spec) for name, spec in specs.items()}
+    bufs = {name: runtime.resident(v) if isinstance(v, np.ndarray) else runtime.alloc(v) for name, v in arrays.items()}
+    jobs = [(kernels[s], [bufs[b] for b in names]) for s, names in plan]
+    if one_at_a_time:
+        for _ in range(repeats):
+            for job in jobs:
+                runtime.execute([job], 1)
+    else:
+        runtime.execute(jobs, repeats)
+    out = {name: runtime.download(b) for name, b in bufs.items()}
+    for b in bufs.values():
+        b.free()
+    return out
+
+
+def test_fused_gate_up_swiglu_is_bit_identical(runtime):
+    # gemm(x, Wg -> G), gemm(x, Wu -> U), swi_glu(G, U -> D) on whole 128x64
+    # tiles run as one fused launch; each of G, U and D must equal the three
+    # jobs launched one at a time, bit for bit.
+    m, n, k = 1024, 3072, 256
+    specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "swiglu": {"op": "swi_glu", "len": m * n}}
+    assert "128x64" in runtime.compile(specs["gemm"]).launch["kernel"]
+    arrays = {"x": orc.normal(m * k, 0x21), "wg": orc.normal(k * n, 0x22, 0.0, 0.1),
+              "wu": orc.normal(k * n, 0x23, 0.0, 0.1), "g": m * n, "u": m * n, "d": m * n}
+    plan = [("gemm", ["x", "wg", "g"]), ("gemm", ["x", "wu", "u"]), ("swiglu", ["g", "u", "d"])]
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
+    for name in ("g", "u", "d"):
+        np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
+    rows = (0, 64)
+    for name, w in (("g", "wg"), ("u", "wu")):
+        want = orc.gemm_reference(m, n, k, arrays["x"], arrays[w], rows=rows)
+        assert orc.compare(fused[name][:64 * n], want, 1e-4, 1e-4).status == 0, name
+    want = orc.swiglu(fused["g"][:64 * n], fused["u"][:64 * n])
+    assert orc.compare(fused["d"][:64 * n], want, 3e-5, 3e-5).status == 0
+
+
+def test_swiglu_writing_a_gemm_input_is_not_fused(runtime):
+    # swi_glu writes the gate weights the GEMMs read (k == m so the lengths
+    # match): fusing would overwrite Wg while other workgroups still read it,
+    # so the batch keeps its order; two repeats make the second read the
+    # overwritten weights.
+    m, n, k = 1024, 3072, 1024
+    specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "swiglu": {"op": "swi_glu", "len": m * n}}
+    arrays = {"x": orc.normal(m * k, 0x31, 0.0, 0.05), "wg": orc.normal(k * n, 0x32, 0.0, 0.05),
+              "wu": orc.normal(k * n, 0x33, 0.0, 0.05), "g": m * n, "u": m * n}
+    plan = [("gemm", ["x", "wg", "g"]), ("gemm", ["x", "wu", "u"]), ("swiglu", ["g", "u", "wg"])]
+    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    ordered = _run_jobs(runtime, specs, arrays, plan, repeats=2, one_at_a_time=True)
+    for name in ("g", "u", "wg"):
+        np.testing.assert_array_equal(batched[name], ordered[name], err_msg=name)
