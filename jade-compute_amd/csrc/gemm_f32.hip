@@ -6,7 +6,8 @@
 // Design (gfx950, wave64):
 //  * Grids of at least 256 whole 256x256 tiles run gemm_f32_mfma_256: one
 //    512-thread workgroup per CU, eight waves of 128x64 (below); a partial last
-//    round of such tiles runs as 128x128 tiles of the kernel below.
+//    round of such tiles runs as 128x128, 128x64 or 64x64 tiles of the kernel
+//    below.
 //  * Otherwise a 256-thread workgroup is a 2x2 grid of waves; each wave owns
 //    TM x TN blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per
 //    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64 or
@@ -456,9 +457,9 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 enum Path { kMixed = 0, kDmaOnly = 1 };
 
 // tail_base >= 0: the launch covers the 256x256 tiles [tail_base, tail_base +
-// gridDim.x / 4) of the grouped order over a tiles_m x tiles_n grid of 256x256
-// tiles, four 128x128 workgroups each (the remainder after the 256x256 kernel's
-// whole rounds).
+// gridDim.x / P) of the grouped order over a tiles_m x tiles_n grid of 256x256
+// tiles, P = (256 / BM) x (256 / BN) workgroups each (the remainder after the
+// 256x256 kernel's whole rounds).
 // pair: a second, independent product of the same shape in the same launch
 // (pair.tiles > 0): positions [tiles, 2*tiles) of the XCD order compute
 // pair.c = pair.a * pair.b.
@@ -496,11 +497,13 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2
         }
         grouped_tile(pos, tiles_m, tiles_n, tm, tn);
     } else if (tail_base >= 0) {
+        constexpr int kSubM = 256 / T::kBM, kSubN = 256 / T::kBN;
         const int pos = xcd_order(int(blockIdx.x), int(gridDim.x));
         int bm, bn;
-        grouped_tile(tail_base + pos / 4, tiles_m, tiles_n, bm, bn);
-        tm = 2 * bm + ((pos >> 1) & 1);
-        tn = 2 * bn + (pos & 1);
+        grouped_tile(tail_base + pos / (kSubM * kSubN), tiles_m, tiles_n, bm, bn);
+        const int sub = pos % (kSubM * kSubN);
+        tm = kSubM * bm + sub / kSubN;
+        tn = kSubN * bn + sub % kSubN;
     } else {
         tile_coords(tiles_m, tiles_n, tm, tn);
     }
@@ -945,6 +948,7 @@ struct Plan {
     int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
     int direct;     // > 0: gemm_f32_direct with this many waves (tiles_m/tiles_n count 32x32 tiles)
     int kgroups;    // 2: 64x64 tiles with two K groups of four waves (0 or 1: one group)
+    int tail_tm, tail_tn;  // big plans: the partial last round's tile, (64*tail_tm) x (64*tail_tn)
 };
 
 constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
@@ -1004,15 +1008,38 @@ int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
     return g;
 }
 
+// The partial last round of a 256x256 grid (`tail` such tiles) runs as
+// 128x128 tiles when those are at most one workgroup per CU, else as the tile
+// among 128x128, 128x64 and 64x64 with the best round fill x efficiency, as
+// for whole grids. Measured with the whole rounds before it: 4096x11008x4096
+// (176 tail tiles) 2868 us with 128x128, 2855 with 128x64; 5120x5120x2048
+// (144) 933 / 874 / 872 with 128x128 / 128x64 / 64x64; 6144x6144x1024 (64)
+// 603 with 128x128 against 630 with 128x64.
+void tail_tile(int tail, int &tm, int &tn) {
+    tm = tn = 2;
+    if (4 * tail <= kCUs) return;
+    const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
+    const double eff[3] = {1.00, 0.97, 0.90};
+    double best = 0.0;
+    for (int i = 0; i < 3; ++i) {
+        const int groups = tail * (4 / shapes[i][0]) * (4 / shapes[i][1]);
+        const int rounds = (groups + kSlots - 1) / kSlots;
+        const double score = eff[i] * double(groups) / double(kSlots * rounds);
+        if (score > best) best = score, tm = shapes[i][0], tn = shapes[i][1];
+    }
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
-        return {4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0, 1};
+        Plan p{4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0, 1, 2, 2};
+        tail_tile(tiles - p.big_full, p.tail_tm, p.tail_tn);
+        return p;
     }
     const int kchunk = int(((k + kBK - 1) / kBK) * kBK);
     auto grid = [&](int tm, int tn) {
         return Plan{tm, tn, 1, kchunk, int((m + 64 * tm - 1) / (64 * tm)), int((n + 64 * tn - 1) / (64 * tn)), false,
-                    0, 0, 1};
+                    0, 0, 1, 0, 0};
     };
     const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
     const double eff[3] = {1.00, 0.97, 0.90};
@@ -1032,7 +1059,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (t > kCUs) return p;
     if (t <= kCUs / 2) {
         if (const int g = direct_waves(m, n, k))
-            return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1};
+            return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1, 0, 0};
         const int want = (kSplitTarget + t - 1) / t;
         const int most = int(k / kMinChunk);
         p.slices = std::max(1, std::min(want, most));
@@ -1075,11 +1102,14 @@ size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
 
 LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    if (p.big)  // the first launch; a partial last round follows as 128x128 tiles
-        return {p.big_full < p.tiles_m * p.tiles_n ? "gemm_f32_mfma_256x256x32_tail128" : "gemm_f32_mfma_256x256x32",
-                {uint32_t(p.big_full), 1, 1},
-                {big::kThreads, 1, 1},
-                big::kLdsBytes};
+    if (p.big) {  // the first launch; a partial last round follows as smaller tiles
+        const char *name = "gemm_f32_mfma_256x256x32";
+        if (p.big_full < p.tiles_m * p.tiles_n)
+            name = p.tail_tm == 1 ? "gemm_f32_mfma_256x256x32_tail64x64"
+                   : p.tail_tn == 1 ? "gemm_f32_mfma_256x256x32_tail128x64"
+                                    : "gemm_f32_mfma_256x256x32_tail128x128";
+        return {name, {uint32_t(p.big_full), 1, 1}, {big::kThreads, 1, 1}, big::kLdsBytes};
+    }
     if (p.direct) {
         static const char *names[3] = {"gemm_f32_direct_32x32x32_w1", "gemm_f32_direct_32x32x32_w2",
                                        "gemm_f32_direct_32x32x32_w4"};
@@ -1166,15 +1196,23 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
             hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.big_full)), dim3(big::kThreads), 0, stream, a, b, c,
                                int(m), int(n), int(k), p.tiles_m, p.tiles_n);
             const int tail = p.tiles_m * p.tiles_n - p.big_full;
-            if (tail > 0)
-                hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), dim3(unsigned(4 * tail)), dim3(kThreads), 0,
-                                   stream, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full,
-                                   PairArgs{});
+            if (tail > 0) {
+                const dim3 grid(unsigned(tail * (4 / p.tail_tm) * (4 / p.tail_tn)));
+                if (p.tail_tm == 1)
+                    hipLaunchKernelGGL((gemm_f32_mfma<1, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
+                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
+                else if (p.tail_tn == 1)
+                    hipLaunchKernelGGL((gemm_f32_mfma<2, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
+                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
+                else
+                    hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
+                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
+            }
             return hipGetLastError();
         }
         // Unaligned pointers: the 128x128 register-staged path (no split: the
         // grid is large).
-        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0, 1};
+        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0, 1, 0, 0};
         launch_tile<2, 2>(stream, q, false, a, b, c, m, n, k);
         return hipGetLastError();
     }
@@ -1182,7 +1220,7 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
         if ((reinterpret_cast<uintptr_t>(a) & 15u) != 0) {
             // Unaligned A: the 64x64 register-staged tiles (no split, no workspace).
-            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0, 1};
+            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0, 1, 0, 0};
             launch_tile<1, 1>(stream, q, false, a, b, c, m, n, k);
         } else if (p.direct == 4) {
             hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,

@@ -150,13 +150,14 @@ def test_two_group_tile_shapes(runtime, m, n, k, kernel):
     gate(got, m, n, k, a, b)
 
 
-@pytest.mark.parametrize("m,n,k,tail", [(4096, 4096, 32, False), (4096, 4096, 96, False), (8192, 8192, 256, False),
-                                         (5120, 5120, 64, True), (6144, 6144, 32, True)])
+@pytest.mark.parametrize("m,n,k,tail", [(4096, 4096, 32, ""), (4096, 4096, 96, ""), (8192, 8192, 256, ""),
+                                         (5120, 5120, 64, "_tail64x64"), (6144, 6144, 32, "_tail128x128"),
+                                         (4096, 11008, 64, "_tail128x64")])
 def test_big_tile_shapes(runtime, m, n, k, tail):
     # The 256x256 eight-wave kernel: one stage, an odd stage count, four rounds,
-    # and grids whose partial last round runs as 128x128 tiles.
+    # and grids whose partial last round runs as 128x128, 128x64 or 64x64 tiles.
     kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
-    want = "gemm_f32_mfma_256x256x32" + ("_tail128" if tail else "")
+    want = "gemm_f32_mfma_256x256x32" + tail
     assert kernel.launch["kernel"] == want, kernel.launch
     a = orc.values(m * k, 0x77, 1.0)
     b = orc.values(k * n, 0x88, 1.0)

@@ -171,7 +171,9 @@ def test_constant_bits_round_trip():
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2", [128, 2, 1]),  # 8 slices per wave: split K
     (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),
     (256, 256, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [16, 16, 1]),
-    (4096, 11008, 4096, "gemm_f32_mfma_256x256x32_tail128", [512, 1, 1]),  # 688 tiles: 2 rounds + 176 as 128x128
+    (4096, 11008, 4096, "gemm_f32_mfma_256x256x32_tail128x64", [512, 1, 1]),  # 688 tiles: 2 rounds + 176 as 128x64
+    (5120, 5120, 2048, "gemm_f32_mfma_256x256x32_tail64x64", [256, 1, 1]),  # 400 tiles: 1 round + 144 as 64x64
+    (6144, 6144, 1024, "gemm_f32_mfma_256x256x32_tail128x128", [512, 1, 1]),  # tail 64: one 128x128 per CU
     (3072, 3072, 3072, "gemm_f32_mfma_64x64x32", [2304, 1, 1]),  # 128x128 would fill 56% of two rounds
     (2500, 2500, 2500, "gemm_f32_mfma_128x128x32", [400, 1, 1]),
     (1024, 4096, 4096, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # 128x64 also for wide C
@@ -180,7 +182,7 @@ def test_constant_bits_round_trip():
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
     # 256x256 for the whole rounds of a grid of >= 256 such tiles (the rest as
-    # 128x128); else the best of 128x128 / 128x64 / 64x64 by round fill x tile
+    # 128x128, 128x64 or 64x64 tiles); else the best of 128x128 / 128x64 / 64x64 by round fill x tile
     # efficiency among grids of >= 384 workgroups; below that 64x64 tiles, with
     # two K groups up to one tile per CU, and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
@@ -210,3 +212,51 @@ def test_materialised_attention_kernels(op, dim, seq, kernel):
     if op == "attention_scores":
         spec["causal"] = True
     assert describe(spec)["launch"]["kernel"] == kernel
+
+
+def _xcd_order(bid, count):
+    # gemm_f32.hip xcd_order: blocks go round-robin over 8 XCDs by id; each
+    # XCD owns a contiguous range of positions.
+    per, rem = divmod(count, 8)
+    xcd, idx = bid % 8, bid // 8
+    return xcd * per + min(xcd, rem) + idx
+
+
+def _grouped_tile(logical, tiles_m, tiles_n, group_m=8):
+    # gemm_f32.hip grouped_tile: 8 tile rows at a time, column-major inside.
+    span = group_m * tiles_n
+    group, inside = divmod(logical, span)
+    first = group * group_m
+    rows = min(tiles_m - first, group_m)
+    return first + inside % rows, inside // rows
+
+
+@pytest.mark.parametrize("m,n,tail_tm,tail_tn", [(4096, 11008, 2, 1), (5120, 5120, 1, 1), (6144, 6144, 2, 2),
+                                                 (4352, 4608, 2, 1)])
+def test_big_plan_covers_every_tile_once(m, n, tail_tm, tail_tn):
+    # The 256x256 launch's whole rounds plus the tail launch in smaller tiles
+    # (the mapping of gemm_f32_mfma_256 and gemm_f32_mfma's tail mode) compute
+    # every 64x64 block of C exactly once.
+    tiles_m, tiles_n = m // 256, n // 256
+    tiles = tiles_m * tiles_n
+    full = tiles // 256 * 256
+    count = {}
+    for bid in range(full):
+        tm, tn = _grouped_tile(_xcd_order(bid, full), tiles_m, tiles_n)
+        for i in range(4):
+            for j in range(4):
+                key = (4 * tm + i, 4 * tn + j)
+                count[key] = count.get(key, 0) + 1
+    sub_m, sub_n = 4 // tail_tm, 4 // tail_tn  # 256 / (64 * tile) per side
+    bm_, bn_ = 64 * tail_tm, 64 * tail_tn
+    groups = (tiles - full) * sub_m * sub_n
+    for bid in range(groups):
+        pos = _xcd_order(bid, groups)
+        bm, bn = _grouped_tile(full + pos // (sub_m * sub_n), tiles_m, tiles_n)
+        sub = pos % (sub_m * sub_n)
+        tm, tn = sub_m * bm + sub // sub_n, sub_n * bn + sub % sub_n
+        for i in range(bm_ // 64):
+            for j in range(bn_ // 64):
+                key = (tm * bm_ // 64 + i, tn * bn_ // 64 + j)
+                count[key] = count.get(key, 0) + 1
+    assert len(count) == (m // 64) * (n // 64) and set(count.values()) == {1}
