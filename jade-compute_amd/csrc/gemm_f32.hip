@@ -454,7 +454,17 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 // writes C + z*M*N, which is then a workspace the reduction kernel consumes.
 // PATH kDmaOnly: every tile of the launch is interior and 16-byte aligned, so
 // only the LDS-direct loop is compiled in (fewer registers, tighter code).
-enum Path { kMixed = 0, kDmaOnly = 1 };
+// kRegOnly: register-staged loads (64-bit addresses) for every tile, for
+// operands too long for the LDS-direct loads' 32-bit offsets.
+enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2 };
+
+// LDS-direct loads address each lane's 16 bytes as a 32-bit byte offset from
+// a wave-uniform base, computed in int: (row * K + 4 * chunk) * 4 for A rows
+// below bm, (row * N + 4 * chunk) * 4 for the 32 B rows of a stage, chunks
+// below bn / 4. Those must stay below 2^31; longer rows take 64-bit loads.
+constexpr bool dma_offsets_fit(uint32_t bm, uint32_t bn, uint32_t k, uint32_t n) {
+    return (uint64_t(bm) * k + kBK) * 4 < (uint64_t(1) << 31) && (uint64_t(kBK) * n + bn) * 4 < (uint64_t(1) << 31);
+}
 
 // tail_base >= 0: the launch covers the 256x256 tiles [tail_base, tail_base +
 // gridDim.x / P) of the grouped order over a tiles_m x tiles_n grid of 256x256
@@ -532,7 +542,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2
     // tiles, unaligned shapes and K ranges that are not KG x nk whole stages
     // take the guarded, register-staged path.
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && klast - kfirst == KG * nk * kBK;
-    if (PATH == kDmaOnly || (VEC && interior))
+    if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
         k_loop_unaligned<TM, TN>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
@@ -985,6 +995,7 @@ constexpr int kMinChunk = 128;
 // one.
 bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     if (m % big::kBM != 0 || n % big::kBN != 0 || k % kBK != 0 || k == 0) return false;
+    if (!dma_offsets_fit(big::kBM, big::kBN, k, n)) return false;
     return uint64_t(m / big::kBM) * (n / big::kBN) >= uint64_t(kCUs);
 }
 
@@ -1073,24 +1084,42 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     return p;
 }
 
+// The 4-wave kernel's load path for a launch: LDS-direct for every tile when
+// all are interior, aligned and within the 32-bit offsets; a per-tile choice
+// when only some are interior; register-staged otherwise.
+Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int tm, int tn, int kg) {
+    if (!vec) return kMixed;  // unaligned: no tile takes the LDS-direct loads
+    if (!dma_offsets_fit(uint32_t(64 * tm), uint32_t(64 * tn), k, n)) return kRegOnly;
+    // Every K slice (the last may be shorter) must be a multiple of KG whole stages.
+    const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
+    const bool all_interior = m % (64 * tm) == 0 && n % (64 * tn) == 0 && chunk % (kBK * kg) == 0 &&
+                              last % (kBK * kg) == 0;
+    return all_interior ? kDmaOnly : kMixed;
+}
+
 template <int TM, int TN, int KG = 1>
 void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
                  uint32_t m, uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
     const unsigned groups = unsigned(p.tiles_m) * unsigned(p.tiles_n) * (pair.tiles > 0 ? 2u : 1u);
     const dim3 grid(groups, unsigned(p.slices)), block(kThreads * KG);
-    // Every K slice (the last may be shorter) must be a multiple of KG whole stages.
-    const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
-    const bool all_interior = vec && m % (64 * TM) == 0 && n % (64 * TN) == 0 && chunk % (kBK * KG) == 0 &&
-                              last % (kBK * KG) == 0;
-    if (all_interior)
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
-                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-    else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out, int(m),
-                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-    else
-        hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out, int(m),
-                           int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+    switch (tile_path(p, vec, m, n, k, TM, TN, KG)) {
+        case kDmaOnly:
+            hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
+                               int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+            break;
+        case kRegOnly:
+            hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kRegOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
+                               int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+            break;
+        default:
+            if (vec)
+                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out,
+                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+            else
+                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out,
+                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+            break;
+    }
 }
 
 }  // namespace
@@ -1161,7 +1190,8 @@ bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
     // outputs are the pair's bits.
     const Plan p = plan_for(m, n, k);
     return !p.big && !p.direct && p.kgroups != 2 && p.slices == 1 && p.tm == 2 && p.tn == 1 &&
-           m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 && k > 0;
+           m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 && k > 0 &&
+           dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
 }
 
 hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,

@@ -165,6 +165,19 @@ def test_big_tile_shapes(runtime, m, n, k, tail):
     gate(got, m, n, k, a, b)
 
 
+def test_long_k_takes_64_bit_loads(runtime):
+    # K long enough that a 64x64 tile's LDS-direct byte offsets (row * K * 4,
+    # a 32-bit offset from a wave-uniform base) would pass 2^31: the launch
+    # must take the register-staged loads with 64-bit addresses. A and B are
+    # 2.3 GB each; the oracle checks two rows (1.1e9 FP64 products).
+    m, n, k = 64, 64, 8912896
+    a = orc.values(m * k, 0x91, 1.0)
+    b = orc.values(k * n, 0x92, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b, rows=(0, 2))
+    assert np.isfinite(got).all()
+
+
 def test_gemm_plan_abi_bench_flow():
     # src/main.rs:281-310 driving src/corex.rs through native/jade_corex.h.
     m = n = k = 512
