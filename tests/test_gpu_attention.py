@@ -155,6 +155,27 @@ def test_split_key_grids(runtime, h, s, d, causal):
     assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
 
 
+# A seeded sample (random.Random(20261202)) of heads <= 12, seq <= 1500 and any
+# head dim <= 128 below 3e8 score products: odd dims (padded to 32/64/128 with
+# scalar loads), ragged query blocks and key tiles, split launches.
+RANDOM_SHAPES = [(3, 1037, 61, False), (1, 618, 122, False), (9, 138, 86, True), (3, 715, 52, True),
+                 (4, 162, 26, False), (5, 550, 110, True), (8, 311, 71, True), (1, 811, 51, True),
+                 (12, 246, 29, False), (9, 661, 42, False), (4, 470, 104, True), (3, 872, 116, True),
+                 (4, 846, 81, True), (2, 1171, 73, False), (3, 418, 19, True), (8, 900, 42, True),
+                 (7, 551, 80, False), (9, 437, 2, False), (10, 548, 7, True), (7, 467, 115, False),
+                 (3, 72, 88, True), (1, 211, 41, True), (7, 426, 77, True), (2, 1252, 16, True)]
+
+
+def test_random_shapes(runtime):
+    for i, (h, s, d, causal) in enumerate(RANDOM_SHAPES):
+        n = h * s * d
+        q, k, v = orc.normal(n, 0x100 + i), orc.normal(n, 0x200 + i), orc.normal(n, 0x300 + i)
+        got = run_online(runtime, h, s, d, causal, q, k, v)
+        want = orc.attention_reference(h, s, d, causal, q, k, v)
+        check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+        assert check.status == 0, ((h, s, d, causal), check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_unsplit_four_wave_grid(runtime, causal):
     h, s, d = 32, 1024, 64  # 256 blocks of 128 queries: no key split

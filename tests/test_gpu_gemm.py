@@ -165,6 +165,39 @@ def test_big_tile_shapes(runtime, m, n, k, tail):
     gate(got, m, n, k, a, b)
 
 
+# A seeded sample (random.Random(20261201)) of shapes below 2e8 products,
+# drawn so that every small- and mid-grid plan family appears: direct-load
+# 32x32 tiles, 64x64 tiles with two K groups (whole or split K), 64x64,
+# 128x64 and 128x128 tiles, aligned and unaligned rows.
+RANDOM_SHAPES = [(511, 305, 479), (139, 175, 471), (79, 931, 359), (50, 156, 7406), (2255, 1803, 4),
+                 (137, 160, 8826), (512, 512, 512), (628, 1002, 247), (128, 256, 1000), (1690, 3463, 30),
+                 (768, 1024, 128), (64, 256, 32), (41, 271, 7183), (2048, 1024, 64), (122, 130, 1844),
+                 (417, 246, 998), (184, 658, 690), (72, 96, 2942), (128, 64, 512), (162, 1832, 90),
+                 (1766, 790, 56), (256, 256, 128), (753, 65, 540), (512, 1024, 256), (1147, 1675, 58),
+                 (2548, 523, 9), (234, 1051, 23), (2174, 761, 69), (2068, 2198, 25), (256, 256, 512),
+                 (729, 20, 93), (2492, 718, 26), (860, 290, 149), (3983, 1198, 21), (131, 164, 96),
+                 (963, 3612, 35), (567, 360, 260), (256, 1024, 64), (128, 512, 256), (985, 362, 249),
+                 (211, 506, 103), (1024, 512, 128), (1989, 3572, 21), (574, 1472, 34), (43, 906, 65),
+                 (64, 512, 64), (653, 249, 224), (1945, 1817, 32), (850, 614, 158), (768, 256, 512),
+                 (351, 694, 504), (1591, 2326, 22), (1933, 3173, 32), (1776, 1805, 47), (3303, 3252, 17),
+                 (2794, 1426, 9), (2078, 1475, 40), (3706, 3196, 3), (1109, 3061, 12), (2638, 1237, 32)]
+
+
+def test_random_shapes_across_plans(runtime):
+    kernels = set()
+    for i, (m, n, k) in enumerate(RANDOM_SHAPES):
+        kernels.add(runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch["kernel"])
+        a = orc.values(m * k, 0x1000 + i, 1.0)
+        b = orc.values(k * n, 0x2000 + i, 1.0)
+        got = run_gemm(runtime, m, n, k, a, b)
+        want = orc.gemm_reference(m, n, k, a, b)
+        check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+        assert check.status == 0, ((m, n, k), check.first_bad, got[check.first_bad], want[check.first_bad])
+    for family in ("direct_32x32x32_w4", "64x64x32_k2", "64x64x32_splitk_k2", "mfma_64x64x32", "128x64x32",
+                   "128x128x32"):
+        assert any(family in name for name in kernels), (family, sorted(kernels))
+
+
 def test_long_k_takes_64_bit_loads(runtime):
     # K long enough that a 64x64 tile's LDS-direct byte offsets (row * K * 4,
     # a 32-bit offset from a wave-uniform base) would pass 2^31: the launch
