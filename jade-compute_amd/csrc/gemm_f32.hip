@@ -485,11 +485,11 @@ struct PairArgs {
 // group runs that many, so the barriers match; stages past the range read
 // zero), each group with its own double-buffered stages in LDS. Groups
 // 1..KG-1 then leave their sums in LDS and group 0 adds them in group order.
-// KG = 2 puts two waves on each SIMD where a grid of 64x64 tiles gives each
-// CU one workgroup, so one wave's barrier and LDS waits overlap the other's
-// matrix work. Not used with pair or tail launches.
+// KG = 2 (4) puts two (four) waves on each SIMD where a grid of 64x64 tiles
+// gives each CU one workgroup, so one wave's barrier and LDS waits overlap
+// the others' matrix work. Not used with pair or tail launches.
 template <int TM, int TN, bool VEC, int PATH, int KG = 1>
-__global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f32_mfma(
+__global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(KG > 2 ? KG : 2, KG > 2 ? KG : 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
     int tiles_m, int tiles_n, int kchunk, int tail_base, PairArgs pair) {
     using T = Tile<TM, TN>;
@@ -957,7 +957,7 @@ struct Plan {
     bool big;       // 256x256 eight-wave tile (tiles_m/tiles_n count 256x256 tiles)
     int big_full;   // 256x256 tiles in whole rounds; the rest run as 128x128 tiles
     int direct;     // > 0: gemm_f32_direct with this many waves (tiles_m/tiles_n count 32x32 tiles)
-    int kgroups;    // 2: 64x64 tiles with two K groups of four waves (0 or 1: one group)
+    int kgroups;    // 2 or 4: 64x64 tiles with that many K groups of four waves (0 or 1: one group)
     int tail_tm, tail_tn;  // big plans: the partial last round's tile, (64*tail_tm) x (64*tail_tn)
 };
 
@@ -966,6 +966,14 @@ constexpr int kMinGroups = 384;    // a tile shape needs ~1.5 workgroups per CU 
 constexpr int kCUs = 256;
 constexpr int kSplitTarget = 256;  // split K into about one workgroup per CU
 constexpr int kMinChunk = 128;
+// Unsplit 64x64 grids of up to one tile per CU with 16-byte rows and K of at
+// least this run four K groups (16 waves, four per SIMD) instead of two.
+// Measured on MI355X: 1024^3 22.8 -> 22.1 us, 1024x1024x2048 42.7 -> 40.5,
+// 1024x1024x4096 82.3 -> 77.4, 1000x1000x1024 25.6 -> 24.5, 768x768x1024
+// 22.6 -> 21.8; K = 512 ties (12.9 / 12.8). The unaligned loop keeps two
+// groups: with two register stages it spills at four waves per SIMD and ran
+// 15% slower (1000x777x513 18.8 -> 21.7 us).
+constexpr int kFourGroupMinK = 768;
 
 // Tile choice among 128x128, 128x64 and 64x64 (128x64 measured at or above
 // 64x128 on the tall and wide shapes tried, so 64x128 is not chosen). Each
@@ -1081,6 +1089,7 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         }
     }
     if (p.kchunk >= 2 * kBK) p.kgroups = 2;
+    if (p.slices == 1 && k % 4 == 0 && n % 4 == 0 && p.kchunk >= kFourGroupMinK) p.kgroups = 4;
     return p;
 }
 
@@ -1148,7 +1157,11 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                 uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
     }
     // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
-    // run two K groups.
+    // run K groups. (A four-group plan whose pointers turn out not 16-byte
+    // aligned launches with two groups.)
+    if (p.kgroups == 4)
+        return {"gemm_f32_mfma_64x64x32_k4", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {4 * kThreads, 1, 1},
+                4 * Tile<1, 1>::kLdsBytes};
     if (p.kgroups == 2)
         return {p.slices > 1 ? "gemm_f32_mfma_64x64x32_splitk_k2" : "gemm_f32_mfma_64x64x32_k2",
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
@@ -1168,13 +1181,13 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
 
 bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    return !p.big && !p.direct && p.kgroups != 2 && p.slices == 1 && m > 0 && n > 0 && k > 0;
+    return !p.big && !p.direct && p.kgroups < 2 && p.slices == 1 && m > 0 && n > 0 && k > 0;
 }
 
 hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
                          const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k) {
     const Plan p = plan_for(m, n, k);
-    if (p.big || p.direct || p.kgroups == 2 || p.slices != 1) return hipErrorInvalidValue;
+    if (p.big || p.direct || p.kgroups >= 2 || p.slices != 1) return hipErrorInvalidValue;
     const uintptr_t bits = reinterpret_cast<uintptr_t>(a0) | reinterpret_cast<uintptr_t>(b0) |
                            reinterpret_cast<uintptr_t>(a1) | reinterpret_cast<uintptr_t>(b1);
     const bool vec = (bits & 15u) == 0 && (k % 4 == 0) && (n % 4 == 0);
@@ -1189,7 +1202,7 @@ bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
     // The plan the pair would take must be the 128x64 tile, so the fused
     // outputs are the pair's bits.
     const Plan p = plan_for(m, n, k);
-    return !p.big && !p.direct && p.kgroups != 2 && p.slices == 1 && p.tm == 2 && p.tn == 1 &&
+    return !p.big && !p.direct && p.kgroups < 2 && p.slices == 1 && p.tm == 2 && p.tn == 1 &&
            m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 && k > 0 &&
            dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
 }
@@ -1265,7 +1278,8 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         return hipGetLastError();
     }
     float *out = p.slices > 1 ? workspace : c;
-    if (p.kgroups == 2) launch_tile<1, 1, 2>(stream, p, vec, a, b, out, m, n, k);
+    if (p.kgroups == 4 && vec) launch_tile<1, 1, 4>(stream, p, vec, a, b, out, m, n, k);
+    else if (p.kgroups >= 2) launch_tile<1, 1, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);
     else launch_tile<1, 1>(stream, p, vec, a, b, out, m, n, k);

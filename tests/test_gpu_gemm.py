@@ -129,9 +129,9 @@ def test_direct_tile_shapes(runtime, m, n, k, waves):
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
-    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 16 per group
+    (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # register-staged (unaligned), last group partial
-    (768, 768, 768, "gemm_f32_mfma_64x64x32_k2"),
+    (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows keep two groups at long K
     (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial
     (65, 67, 63, "gemm_f32_mfma_64x64x32_k2"),  # one stage per group
     (100, 100, 40, "gemm_f32_mfma_64x64x32_k2"),  # group 1's stage lies mostly past K
@@ -146,6 +146,25 @@ def test_two_group_tile_shapes(runtime, m, n, k, kernel):
     assert launch["kernel"] == kernel, launch
     a = orc.values(m * k, 0xBB, 1.0)
     b = orc.values(k * n, 0xCC, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    gate(got, m, n, k, a, b)
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1024, 1024, 1024),  # LDS-direct stages, 8 per group
+    (768, 768, 768),  # 6 stages per group
+    (1000, 1000, 1024),  # edge tiles register-staged (16-byte rows), interior LDS-direct
+    (1000, 600, 1000),  # 32 stages, the last partial: every tile register-staged
+    (768, 768, 2048),  # 16 stages per group
+])
+def test_four_group_tile_shapes(runtime, m, n, k):
+    # 64x64 tiles whose four K groups of four waves each sum a quarter of the
+    # workgroup's K range; groups 1-3 leave their sums in LDS and group 0 adds
+    # them in group order.
+    launch = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch
+    assert launch["kernel"] == "gemm_f32_mfma_64x64x32_k4" and launch["block"] == [1024, 1, 1], launch
+    a = orc.values(m * k, 0xBD, 1.0)
+    b = orc.values(k * n, 0xCE, 1.0)
     got = run_gemm(runtime, m, n, k, a, b, repeats=2)
     gate(got, m, n, k, a, b)
 

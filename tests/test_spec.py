@@ -161,12 +161,14 @@ def test_constant_bits_round_trip():
     (8192, 8192, 256, "gemm_f32_mfma_256x256x32", [1024, 1, 1]),
     (4096, 4096, 4112, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # K not a multiple of 32
     (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
-    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k2", [256, 1, 1]),  # <= 256 tiles: two K groups per tile
+    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, aligned, K >= 768: four K groups
+    (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2", [256, 1, 1]),  # shorter K: two K groups
+    (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),  # unaligned rows: two K groups
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),
     (1536, 1024, 1024, "gemm_f32_mfma_64x64x32", [384, 1, 1]),  # 256 < tiles < 384: one group
     (512, 512, 512, "gemm_f32_direct_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K
     (700, 700, 700, "gemm_f32_direct_32x32x32_w4", [484, 1, 1]),  # 6 slices per wave
-    (768, 768, 768, "gemm_f32_mfma_64x64x32_k2", [144, 1, 1]),  # > 128 64x64 tiles: not direct
+    (768, 768, 768, "gemm_f32_mfma_64x64x32_k4", [144, 1, 1]),  # > 128 64x64 tiles: not direct
     (255, 257, 4, "gemm_f32_direct_32x32x32_w1", [72, 1, 1]),  # one slice: one wave
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2", [128, 2, 1]),  # 8 slices per wave: split K
     (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),
@@ -184,7 +186,8 @@ def test_gemm_launch_plans(m, n, k, kernel, grid):
     # 256x256 for the whole rounds of a grid of >= 256 such tiles (the rest as
     # 128x128, 128x64 or 64x64 tiles); else the best of 128x128 / 128x64 / 64x64 by round fill x tile
     # efficiency among grids of >= 384 workgroups; below that 64x64 tiles, with
-    # two K groups up to one tile per CU, and at most half the CUs' worth of
+    # two K groups up to one tile per CU (four for aligned rows and K >= 768),
+    # and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
     assert launch["kernel"] == kernel and launch["grid"] == grid, launch
