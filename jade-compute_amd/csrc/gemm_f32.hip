@@ -401,6 +401,66 @@ __device__ inline void store_stage_masked(float *stage, const Regs<TM, TN> &r, i
     }
 }
 
+// Writes a whole stage (k0 + 32 <= kend): no masks.
+template <int TM, int TN>
+__device__ inline void store_stage_plain(float *stage, const Regs<TM, TN> &r, int t) {
+    using T = Tile<TM, TN>;
+    float *as = stage, *bs = stage + T::kAStage;
+#pragma unroll
+    for (int j = 0; j < T::kBM * kBK / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        as[(f / kBK) * kLDA + f % kBK] = r.a[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kBK * T::kBN / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        bs[(f / T::kBN) * T::kLDB + f % T::kBN] = r.b[j];
+    }
+}
+
+// Buffer loads for unaligned operands below 2 GiB: each lane keeps a 32-bit
+// byte offset per element of the stage at kbegin (rows of A past M and
+// columns of B past N clamped once), and a stage is that offset plus a
+// uniform step. The buffer's range check returns zero for offsets past the
+// operand's end, so the loads past K need no clamps; the k >= kend mask of
+// store_stage_masked still applies to a group's partial last stage.
+constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
+template <int TM, int TN>
+struct BufOffsets {
+    uint32_t a[Tile<TM, TN>::kBM * kBK / kThreads], b[kBK * Tile<TM, TN>::kBN / kThreads];
+};
+
+template <int TM, int TN>
+__device__ inline void buffer_offsets(int M, int N, int K, int m0, int n0, int kbegin, int t,
+                                      BufOffsets<TM, TN> &o) {
+    using T = Tile<TM, TN>;
+#pragma unroll
+    for (int j = 0; j < T::kBM * kBK / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        o.a[j] = (uint32_t(min(m0 + f / kBK, M - 1)) * uint32_t(K) + uint32_t(kbegin + f % kBK)) * 4u;
+    }
+#pragma unroll
+    for (int j = 0; j < kBK * T::kBN / kThreads; ++j) {
+        const int f = t + j * kThreads;
+        o.b[j] = (uint32_t(kbegin + f / T::kBN) * uint32_t(N) + uint32_t(min(n0 + f % T::kBN, N - 1))) * 4u;
+    }
+}
+
+// Stage s of the range (k0 = kbegin + 32 s): A advances 128 bytes per stage,
+// B 32 rows.
+template <int TM, int TN>
+__device__ inline void load_stage_buffer(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
+                                         const BufOffsets<TM, TN> &o, uint32_t astep, uint32_t bstep,
+                                         Regs<TM, TN> &r) {
+    using T = Tile<TM, TN>;
+#pragma unroll
+    for (int j = 0; j < T::kBM * kBK / kThreads; ++j)
+        r.a[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, int(o.a[j] + astep), 0, 0));
+#pragma unroll
+    for (int j = 0; j < kBK * T::kBN / kThreads; ++j)
+        r.b[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(o.b[j] + bstep), 0, 0));
+}
+
 // A barrier that orders LDS only: this wave's LDS reads and writes complete
 // before it, global loads stay in flight across it. __syncthreads() carries a
 // workgroup release fence, for which the compiler also waits for every
@@ -410,17 +470,40 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 
 // `nk` stages from kbegin; stage kt+2's loads are issued while stage kt is
 // consumed and stage kt+1 (loaded an iteration earlier) is written to LDS.
-template <int TM, int TN>
+// BUF: buffer loads (operands below 2 GiB); else clamped global loads.
+template <int TM, int TN, bool BUF>
 __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float *__restrict__ B, float *smem,
                                         int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
                                         int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     Regs<TM, TN> r[2];
-    load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin, r[0], t);
+    BufOffsets<TM, TN> off;
+    __amdgpu_buffer_rsrc_t ra, rb;
+    if (BUF) {
+        ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, int(uint32_t(M) * uint32_t(K) * 4u),
+                                               int(kBufferWord3));
+        rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(B), 0, int(uint32_t(K) * uint32_t(N) * 4u),
+                                               int(kBufferWord3));
+        buffer_offsets<TM, TN>(M, N, K, m0, n0, kbegin, t, off);
+    }
+    const uint32_t bstage = uint32_t(kBK) * uint32_t(N) * 4u;
+    auto load = [&](int s, Regs<TM, TN> &dst) {
+        if (BUF)
+            load_stage_buffer<TM, TN>(ra, rb, off, uint32_t(s) * (kBK * 4u), uint32_t(s) * bstage, dst);
+        else
+            load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + s * kBK, dst, t);
+    };
+    auto store = [&](float *stage, const Regs<TM, TN> &src, int k0) {
+        if (k0 + kBK <= kend)  // block-uniform
+            store_stage_plain<TM, TN>(stage, src, t);
+        else
+            store_stage_masked<TM, TN>(stage, src, k0, kend, t);
+    };
+    load(0, r[0]);
     __builtin_amdgcn_sched_barrier(0);
-    load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + kBK, r[1], t);
+    load(1, r[1]);
     __builtin_amdgcn_sched_barrier(0);
-    store_stage_masked<TM, TN>(smem, r[0], kbegin, kend, t);
+    store(smem, r[0], kbegin);
     lds_barrier();
     // Unrolled by two so the register stage in use is a compile-time index.
     for (int kt = 0; kt < nk; kt += 2) {
@@ -431,8 +514,8 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 const float *cur = smem + u * T::kStage;
                 // Unconditional, so every path into the loop has the same
                 // loads in flight and the waits below stay exact; stages past
-                // nk load clamped, in-bounds data that is never stored.
-                load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + (k + 2) * kBK, r[u], t);
+                // nk load in-bounds (or range-checked) data that is never stored.
+                load(k + 2, r[u]);
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16 part[TM][TN];
                 mma_stage<TM, TN>(cur, wm, wn, lane, part);
@@ -440,8 +523,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-                if (k + 1 < nk)
-                    store_stage_masked<TM, TN>(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK, kend, t);
+                if (k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
                 lds_barrier();
             }
         }
@@ -456,7 +538,9 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 // only the LDS-direct loop is compiled in (fewer registers, tighter code).
 // kRegOnly: register-staged loads (64-bit addresses) for every tile, for
 // operands too long for the LDS-direct loads' 32-bit offsets.
-enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2 };
+// kUnalignedBuf: unaligned rows (no 16-byte loads) through buffer loads,
+// for 64x64 and 128x64 tiles over operands below 2 GiB each.
+enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2, kUnalignedBuf = 3 };
 
 // LDS-direct loads address each lane's 16 bytes as a 32-bit byte offset from
 // a wave-uniform base, computed in int: (row * K + 4 * chunk) * 4 for A rows
@@ -545,7 +629,8 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
-        k_loop_unaligned<TM, TN>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
+        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane,
+                                                       t, acc);
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
@@ -1097,7 +1182,10 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
 // all are interior, aligned and within the 32-bit offsets; a per-tile choice
 // when only some are interior; register-staged otherwise.
 Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int tm, int tn, int kg) {
-    if (!vec) return kMixed;  // unaligned: no tile takes the LDS-direct loads
+    if (!vec) {  // unaligned: no tile takes the LDS-direct loads
+        const bool buffers = uint64_t(m) * k * 4 < (uint64_t(1) << 31) && uint64_t(k) * n * 4 < (uint64_t(1) << 31);
+        return buffers && tm * tn <= 2 ? kUnalignedBuf : kMixed;
+    }
     if (!dma_offsets_fit(uint32_t(64 * tm), uint32_t(64 * tn), k, n)) return kRegOnly;
     // Every K slice (the last may be shorter) must be a multiple of KG whole stages.
     const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
@@ -1120,11 +1208,16 @@ void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, co
             hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kRegOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
                                int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
             break;
+        case kUnalignedBuf:
+            if constexpr (TM * TN <= 2 && KG <= 2)
+                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kUnalignedBuf, KG>), grid, block, 0, stream, a, b, out,
+                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+            break;
         default:
             if (vec)
                 hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out,
                                    int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-            else
+            else if constexpr (KG <= 2)  // four-group plans launch with two groups when unaligned
                 hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out,
                                    int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
             break;

@@ -230,6 +230,19 @@ def test_long_k_takes_64_bit_loads(runtime):
     assert np.isfinite(got).all()
 
 
+def test_unaligned_operand_above_2_gib_takes_global_loads(runtime):
+    # Unaligned rows (K % 4 != 0) normally load through buffer instructions
+    # with 32-bit offsets and the buffer's range check; an operand of 2 GiB or
+    # more (A here: 64 x 8388609 floats) must take the clamped 64-bit global
+    # loads instead. The oracle checks the last two rows.
+    m, n, k = 64, 3, 8388609
+    a = orc.values(m * k, 0x93, 1.0)
+    b = orc.values(k * n, 0x94, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b, rows=(62, 64))
+    assert np.isfinite(got).all()
+
+
 def test_gemm_plan_abi_bench_flow():
     # src/main.rs:281-310 driving src/corex.rs through native/jade_corex.h.
     m = n = k = 512
