@@ -216,18 +216,20 @@ __device__ inline void store_stage(float *stage, const f32x4 (&ra)[Tile<TM, TN>:
 // One K stage into fresh accumulators; the caller adds the stage sums into the
 // running totals with VALU adds, so the long K recurrence is 1 add per 32 k
 // instead of 16 chained matrix-core accumulations per 32 k.
-template <int TM, int TN>
+template <int TM, int TN, bool ZERO = true>
 __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
     const float *ap = stage + (wm * 32 * TM + c) * kLDA + 16 * h;
     const float *bp = stage + T::kAStage + (16 * h) * T::kLDB + wn * 32 * TN + c;
+    if (ZERO) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         f32x4 a[TM];
@@ -249,17 +251,20 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
 }
 
 // mma_stage over the swizzled layout: A stage at `as`, B stage at `bs`.
-template <int TM, int TN>
+// ZERO: start the sums at zero; otherwise add onto `acc`.
+template <int TM, int TN, bool ZERO = true>
 __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, int wn, int lane,
                                      f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
+    if (ZERO) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         f32x4 a[TM];
@@ -289,6 +294,7 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // The K loop for interior tiles: LDS-direct loads of stage kt+1 run while the
 // matrix cores consume stage kt; each wave drains its own loads, then one
 // barrier publishes the stage and retires the buffer the next loads overwrite.
+// The matrix cores sum two stages into `part` before each fold into acc.
 // `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
 // group (every group of a workgroup runs the same number of stages, so the
 // barriers match).
@@ -301,24 +307,36 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
     issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin, lds0, t);
     drain_vmem();
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * T::kStageS;
-        if (kt + 1 < nk)
-            issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin + (kt + 1) * kBK,
-                                    lds0 + uint32_t(((kt + 1) & 1) * T::kStageS * 4), t);
-        // Raised wave priority while this wave has matrix work, so the SIMD's
-        // arbiter favours it over the co-resident workgroup's loads and folds
-        // (measured +1-2% at 4096^3).
-        __builtin_amdgcn_s_setprio(1);
-        f32x16 part[TM][TN];
-        mma_stage_swz<TM, TN>(cur, cur + T::kAStageS, wm, wn, lane, part);
+    // Partial sums run over two stages (64 k) before each fold into acc.
+    f32x16 part[TM][TN];
+    for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int u = 0; u < 2; ++u) {
+            const int k = kt + u;
+            if (k < nk) {  // block-uniform
+                const float *cur = smem + u * T::kStageS;
+                if (k + 1 < nk)
+                    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
+                                            lds0 + uint32_t((1 - u) * T::kStageS * 4), t);
+                // Raised wave priority while this wave has matrix work, so the
+                // SIMD's arbiter favours it over the co-resident workgroup's
+                // loads and folds (measured +1-2% at 4096^3).
+                __builtin_amdgcn_s_setprio(1);
+                if (u == 0)
+                    mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part);
+                else
+                    mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part);
+                if (u == 1 || k + 1 == nk) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-        __builtin_amdgcn_s_setprio(0);
-        drain_vmem();
-        __syncthreads();
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+                }
+                __builtin_amdgcn_s_setprio(0);
+                drain_vmem();
+                __syncthreads();
+            }
+        }
     }
 }
 
@@ -334,19 +352,34 @@ __device__ inline void k_loop(const float *__restrict__ A, const float *__restri
     load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin, ra, rb, t);
     store_stage<TM, TN>(smem, ra, rb, t);
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * T::kStage;
-        float *nxt = smem + ((kt + 1) & 1) * T::kStage;
-        const bool more = kt + 1 < nk;
-        if (more) load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin + (kt + 1) * kBK, ra, rb, t);
-        f32x16 part[TM][TN];
-        mma_stage<TM, TN>(cur, wm, wn, lane, part);
+    // Partial sums run over two stages (64 k) before each fold into acc,
+    // except at 128x128, whose register-staged loop would then spill.
+    constexpr bool kPairs = TM * TN <= 2;
+    f32x16 part[TM][TN];
+    for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int u = 0; u < 2; ++u) {
+            const int k = kt + u;
+            if (k < nk) {  // block-uniform
+                const float *cur = smem + u * T::kStage;
+                float *nxt = smem + (1 - u) * T::kStage;
+                const bool more = k + 1 < nk;
+                if (more)
+                    load_stage<TM, TN, VEC, GUARD>(A, B, M, N, K, kend, m0, n0, kbegin + (k + 1) * kBK, ra, rb, t);
+                if (u == 0 || !kPairs)
+                    mma_stage<TM, TN, true>(cur, wm, wn, lane, part);
+                else
+                    mma_stage<TM, TN, false>(cur, wm, wn, lane, part);
+                if (u == 1 || !more || !kPairs) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-        if (more) store_stage<TM, TN>(nxt, ra, rb, t);
-        __syncthreads();
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+                }
+                if (more) store_stage<TM, TN>(nxt, ra, rb, t);
+                __syncthreads();
+            }
+        }
     }
 }
 
@@ -506,6 +539,8 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
     store(smem, r[0], kbegin);
     lds_barrier();
     // Unrolled by two so the register stage in use is a compile-time index.
+    // Each stage folds its own partial sums (a fold every two stages, as in
+    // the other loops, measured 5% slower here).
     for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -737,19 +772,31 @@ __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
     dual::issue_stage(A, B, N, K, m0, n0, 0, lds0, wave, lane);
     drain_vmem();
     __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const float *cur = smem + (kt & 1) * kStage;
-        if (kt + 1 < nk)
-            dual::issue_stage(A, B, N, K, m0, n0, (kt + 1) * kBK, lds0 + uint32_t(((kt + 1) & 1) * kStage * 4), wave,
-                              lane);
-        __builtin_amdgcn_s_setprio(1);
-        f32x16 part[2][1];
-        mma_stage_swz<2, 1>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+    // The 128x64 kernel's schedule: partial sums over two stages, then a fold.
+    f32x16 part[2][1];
+    for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[i][0] += part[i][0];
-        __builtin_amdgcn_s_setprio(0);
-        drain_vmem();
-        __syncthreads();
+        for (int u = 0; u < 2; ++u) {
+            const int k = kt + u;
+            if (k < nk) {
+                const float *cur = smem + u * kStage;
+                if (k + 1 < nk)
+                    dual::issue_stage(A, B, N, K, m0, n0, (k + 1) * kBK, lds0 + uint32_t((1 - u) * kStage * 4), wave,
+                                      lane);
+                __builtin_amdgcn_s_setprio(1);
+                if (u == 0)
+                    mma_stage_swz<2, 1, true>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+                else
+                    mma_stage_swz<2, 1, false>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+                if (u == 1 || k + 1 == nk) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) acc[i][0] += part[i][0];
+                }
+                __builtin_amdgcn_s_setprio(0);
+                drain_vmem();
+                __syncthreads();
+            }
+        }
     }
     // The loop ended on a barrier: the stage buffers are free for U.
     const int h = lane >> 5, c = lane & 31;
@@ -784,9 +831,9 @@ __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
 // per CU (two 64 KiB stages), waves 2 (M) x 4 (N), each
 // wave 4x2 MFMA blocks. A stage's B operands for both column blocks are read
 // once (32 registers), then each row block runs two 16-deep MFMA chains into
-// fresh accumulators and folds them into the running sums, so the per-stage
-// accumulation is the same two-level scheme as the smaller tiles (bit-identical
-// results) while only two blocks' partial sums are live. Per stage each wave
+// fresh accumulators and folds them into the running sums while the next
+// block's chains run, so only two blocks' partial sums are live (a fold every
+// stage, where the smaller LDS-direct tiles fold every two). Per stage each wave
 // issues 128 MFMAs against 16 ds_read_b128 and 16 ds_read2_b32, against 64
 // MFMAs per 8 + 16 for the 64x64 wave tile. Interior tiles only: M and N
 // multiples of 256, K a multiple of 32, 16-byte aligned rows.
