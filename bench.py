@@ -295,10 +295,10 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
 
 # Shapes for MFMA-utilisation counter runs: each launch keeps the summed
 # SQ_VALU_MFMA_BUSY_CYCLES below the 2^31 at which the counter saturates, and
-# each exercises one production kernel (256x256 and 128x64 GEMM tiles, 64x64
-# tiles with two K groups, direct-load 32x32 tiles; the split-key, four-wave and
-# eight-wave attention launches).
-MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024), (512, 512, 512))
+# each exercises one production kernel (128x128 and 128x64 GEMM tiles, 64x64
+# tiles with four K groups, direct-load 32x32 tiles, the 256x256 tile with a
+# 64x64 tail; the split-key, four-wave and eight-wave attention launches).
+MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024), (512, 512, 512), (5120, 5120, 1024))
 MFMA_ATTENTION = ((8, 1024, 64, False), (8, 1024, 64, True), (32, 2048, 64, True), (64, 2048, 128, True))
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 XCDS = 8

@@ -1126,13 +1126,16 @@ constexpr int kFourGroupMinK = 768;
 //    ordered reduction: 1024x512x1024 25.2 us unsplit, 16.7 split in two;
 //    512x1024x2048 48.3 -> 25.8. A K group needs two stages or more.
 
-// The 256x256 tile runs one workgroup per CU, so it takes the whole rounds of
-// 256 tiles of a grid of 256x256 tiles; the rest of the grid (a partial round)
-// runs as 128x128 tiles, two workgroups per CU. Measured on MI355X with the
-// 256x256 kernel alone: 4096^3 (256 tiles) 135.9 against 127.2 TFLOP/s for
-// 128x128, 8192x8192x4096 (1024) 136.4 against 128.5, but 4096x11008x4096
-// (688 tiles, 2.69 rounds) 121.8 against 125.4: a partial round costs a whole
-// one.
+// Grids of at least 256 tiles of 256x256 run as 128x128 tiles (two
+// workgroups per CU, each with its own barrier, folding every two stages)
+// unless that grid's last round would hold fewer than 128 of its 512
+// workgroups. Measured on MI355X, 128x128 against the 256x256 kernel (plus a
+// tail in smaller tiles): 4096^3 136.6 / 135.2 TFLOP/s, 8192x8192x2048 136.4 /
+// 134.7, 4096x4096x16384 138.6 / 136.4, 4096x11008x4096 (5.4 rounds) 133.5 /
+// 131.3, 6144x6144x2048 (4.5) 135.0 / 132.9; but 5120x5120x2048 (3.1 rounds)
+// 120.4 / 126.3. There the 256x256 tile (one workgroup per CU) takes the whole
+// rounds of 256 tiles and the rest of the grid (a partial round) runs as
+// smaller tiles: a partial round costs about a whole one.
 bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     if (m % big::kBM != 0 || n % big::kBN != 0 || k % kBK != 0 || k == 0) return false;
     if (!dma_offsets_fit(big::kBM, big::kBN, k, n)) return false;
@@ -1183,6 +1186,8 @@ void tail_tile(int tail, int &tm, int &tn) {
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
+        if ((4 * tiles) % kSlots == 0 || (4 * tiles) % kSlots >= kSlots / 4)
+            return Plan{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0, 1, 0, 0};
         Plan p{4, 4, 1, int(k), int(m / big::kBM), int(n / big::kBN), true, tiles / kCUs * kCUs, 0, 1, 2, 2};
         tail_tile(tiles - p.big_full, p.tail_tm, p.tail_tn);
         return p;

@@ -169,14 +169,19 @@ def test_four_group_tile_shapes(runtime, m, n, k):
     gate(got, m, n, k, a, b)
 
 
-@pytest.mark.parametrize("m,n,k,tail", [(4096, 4096, 32, ""), (4096, 4096, 96, ""), (8192, 8192, 256, ""),
-                                         (5120, 5120, 64, "_tail64x64"), (6144, 6144, 32, "_tail128x128"),
-                                         (4096, 11008, 64, "_tail128x64")])
-def test_big_tile_shapes(runtime, m, n, k, tail):
-    # The 256x256 eight-wave kernel: one stage, an odd stage count, four rounds,
-    # and grids whose partial last round runs as 128x128, 128x64 or 64x64 tiles.
+@pytest.mark.parametrize("m,n,k,want", [
+    (4096, 4096, 32, "gemm_f32_mfma_128x128x32"),  # one stage
+    (4096, 4096, 96, "gemm_f32_mfma_128x128x32"),  # odd stage count: the last two-stage run holds one
+    (8192, 8192, 256, "gemm_f32_mfma_128x128x32"),  # eight rounds
+    (4096, 11008, 64, "gemm_f32_mfma_128x128x32"),  # 5.4 rounds
+    (5120, 5120, 64, "gemm_f32_mfma_256x256x32_tail64x64"),
+    (4352, 4096, 32, "gemm_f32_mfma_256x256x32_tail128x128"),
+])
+def test_large_grid_shapes(runtime, m, n, k, want):
+    # Grids of at least 256 tiles of 256x256: whole rounds of 128x128 tiles,
+    # or, where that grid's last round would be under a quarter full, the
+    # 256x256 eight-wave kernel for whole rounds plus a tail in smaller tiles.
     kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
-    want = "gemm_f32_mfma_256x256x32" + tail
     assert kernel.launch["kernel"] == want, kernel.launch
     a = orc.values(m * k, 0x77, 1.0)
     b = orc.values(k * n, 0x88, 1.0)

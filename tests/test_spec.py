@@ -157,8 +157,8 @@ def test_constant_bits_round_trip():
 
 
 @pytest.mark.parametrize("m,n,k,kernel,grid", [
-    (4096, 4096, 4096, "gemm_f32_mfma_256x256x32", [256, 1, 1]),
-    (8192, 8192, 256, "gemm_f32_mfma_256x256x32", [1024, 1, 1]),
+    (4096, 4096, 4096, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # >= 256 tiles of 256x256: whole 128x128 rounds
+    (8192, 8192, 256, "gemm_f32_mfma_128x128x32", [4096, 1, 1]),
     (4096, 4096, 4112, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # K not a multiple of 32
     (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, aligned, K >= 768: four K groups
@@ -173,9 +173,10 @@ def test_constant_bits_round_trip():
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2", [128, 2, 1]),  # 8 slices per wave: split K
     (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),
     (256, 256, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [16, 16, 1]),
-    (4096, 11008, 4096, "gemm_f32_mfma_256x256x32_tail128x64", [512, 1, 1]),  # 688 tiles: 2 rounds + 176 as 128x64
-    (5120, 5120, 2048, "gemm_f32_mfma_256x256x32_tail64x64", [256, 1, 1]),  # 400 tiles: 1 round + 144 as 64x64
-    (6144, 6144, 1024, "gemm_f32_mfma_256x256x32_tail128x128", [512, 1, 1]),  # tail 64: one 128x128 per CU
+    (4096, 11008, 4096, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),  # 128x128 last round 192/512 full
+    (5120, 5120, 2048, "gemm_f32_mfma_256x256x32_tail64x64", [256, 1, 1]),  # 128x128 last round 64/512: 256x256 + tail
+    (4352, 4096, 1024, "gemm_f32_mfma_256x256x32_tail128x128", [256, 1, 1]),  # tail 16: one 128x128 per CU
+    (6144, 6144, 1024, "gemm_f32_mfma_128x128x32", [2304, 1, 1]),
     (3072, 3072, 3072, "gemm_f32_mfma_64x64x32", [2304, 1, 1]),  # 128x128 would fill 56% of two rounds
     (2500, 2500, 2500, "gemm_f32_mfma_128x128x32", [400, 1, 1]),
     (1024, 4096, 4096, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # 128x64 also for wide C
@@ -183,8 +184,10 @@ def test_constant_bits_round_trip():
     (4096, 2816, 1024, "gemm_f32_mfma_128x64x32", [1408, 1, 1]),  # MLP gate/up
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
-    # 256x256 for the whole rounds of a grid of >= 256 such tiles (the rest as
-    # 128x128, 128x64 or 64x64 tiles); else the best of 128x128 / 128x64 / 64x64 by round fill x tile
+    # Grids of >= 256 tiles of 256x256 as 128x128 tiles, unless that grid's
+    # last round would be under a quarter full: then 256x256 for the whole
+    # rounds (the rest as 128x128, 128x64 or 64x64 tiles); else the best of
+    # 128x128 / 128x64 / 64x64 by round fill x tile
     # efficiency among grids of >= 384 workgroups; below that 64x64 tiles, with
     # two K groups up to one tile per CU (four for aligned rows and K >= 768),
     # and at most half the CUs' worth of
