@@ -1163,24 +1163,15 @@ int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
 }
 
 // The partial last round of a 256x256 grid (`tail` such tiles) runs as
-// 128x128 tiles when those are at most one workgroup per CU, else as the tile
-// among 128x128, 128x64 and 64x64 with the best round fill x efficiency, as
-// for whole grids. Measured with the whole rounds before it: 4096x11008x4096
-// (176 tail tiles) 2868 us with 128x128, 2855 with 128x64; 5120x5120x2048
-// (144) 933 / 874 / 872 with 128x128 / 128x64 / 64x64; 6144x6144x1024 (64)
-// 603 with 128x128 against 630 with 128x64.
+// 128x128 tiles when those are at most one workgroup per CU, else as 64x64
+// tiles. Measured with the whole rounds before it: 5120x5120x2048 (144 tail
+// tiles) 933 / 874 / 872 us with 128x128 / 128x64 / 64x64; 6144x6144x1024 (64)
+// 603 with 128x128 against 630 with 128x64. (A grid takes the 256x256 plan
+// only when its 128x128 last round would be under a quarter full, so the
+// tail is 1-31 or 129-159 tiles, where 64x64 tiles fill the rounds better
+// than 128x64 ones by the fill x efficiency measure of the whole-grid choice.)
 void tail_tile(int tail, int &tm, int &tn) {
-    tm = tn = 2;
-    if (4 * tail <= kCUs) return;
-    const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
-    const double eff[3] = {1.00, 0.97, 0.90};
-    double best = 0.0;
-    for (int i = 0; i < 3; ++i) {
-        const int groups = tail * (4 / shapes[i][0]) * (4 / shapes[i][1]);
-        const int rounds = (groups + kSlots - 1) / kSlots;
-        const double score = eff[i] * double(groups) / double(kSlots * rounds);
-        if (score > best) best = score, tm = shapes[i][0], tn = shapes[i][1];
-    }
+    tm = tn = 4 * tail <= kCUs ? 2 : 1;
 }
 
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
@@ -1288,9 +1279,7 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     if (p.big) {  // the first launch; a partial last round follows as smaller tiles
         const char *name = "gemm_f32_mfma_256x256x32";
         if (p.big_full < p.tiles_m * p.tiles_n)
-            name = p.tail_tm == 1 ? "gemm_f32_mfma_256x256x32_tail64x64"
-                   : p.tail_tn == 1 ? "gemm_f32_mfma_256x256x32_tail128x64"
-                                    : "gemm_f32_mfma_256x256x32_tail128x128";
+            name = p.tail_tm == 1 ? "gemm_f32_mfma_256x256x32_tail64x64" : "gemm_f32_mfma_256x256x32_tail128x128";
         return {name, {uint32_t(p.big_full), 1, 1}, {big::kThreads, 1, 1}, big::kLdsBytes};
     }
     if (p.direct) {
@@ -1388,9 +1377,6 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
                 const dim3 grid(unsigned(tail * (4 / p.tail_tm) * (4 / p.tail_tn)));
                 if (p.tail_tm == 1)
                     hipLaunchKernelGGL((gemm_f32_mfma<1, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
-                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
-                else if (p.tail_tn == 1)
-                    hipLaunchKernelGGL((gemm_f32_mfma<2, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
                                        int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
                 else
                     hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
