@@ -41,6 +41,7 @@
 #include "ops.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace jade {
 namespace hipk {
@@ -451,31 +452,40 @@ __device__ inline void store_stage_plain(float *stage, const Regs<TM, TN> &r, in
     }
 }
 
-// Buffer loads for unaligned operands below 2 GiB: each lane keeps a 32-bit
-// byte offset per element of the stage at kbegin (rows of A past M and
-// columns of B past N clamped once), and a stage is that offset plus a
-// uniform step. The buffer's range check returns zero for offsets past the
-// operand's end, so the loads past K need no clamps; the k >= kend mask of
-// store_stage_masked still applies to a group's partial last stage.
+// Buffer loads for unaligned operands below 2 GiB. Each lane loads the same
+// 16-byte runs as the aligned register path (store_stage's layout: four
+// consecutive k of an A row, four consecutive columns of a B row), but at
+// 4-byte-aligned offsets, which buffer loads take. Each lane keeps one 32-bit
+// byte offset per run of the stage at kbegin (rows of A past M clamped once),
+// and a stage is that offset plus a uniform step. The buffer's range check
+// returns zero for any part of a run past the operand's end, so no load is
+// clamped along K or N: a run that crosses the end of a B row reads the next
+// row's first floats into columns past N, which no output keeps, and k >=
+// kend is zeroed when a group's partial last stage is written to LDS.
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
 template <int TM, int TN>
 struct BufOffsets {
-    uint32_t a[Tile<TM, TN>::kBM * kBK / kThreads], b[kBK * Tile<TM, TN>::kBN / kThreads];
+    uint32_t a[Tile<TM, TN>::kALoads], b[Tile<TM, TN>::kBLoads];
+};
+template <int TM, int TN>
+struct Regs4 {
+    f32x4 a[Tile<TM, TN>::kALoads], b[Tile<TM, TN>::kBLoads];
 };
 
 template <int TM, int TN>
 __device__ inline void buffer_offsets(int M, int N, int K, int m0, int n0, int kbegin, int t,
                                       BufOffsets<TM, TN> &o) {
     using T = Tile<TM, TN>;
+    constexpr int kRowF4 = T::kBN / 4;
 #pragma unroll
-    for (int j = 0; j < T::kBM * kBK / kThreads; ++j) {
-        const int f = t + j * kThreads;
-        o.a[j] = (uint32_t(min(m0 + f / kBK, M - 1)) * uint32_t(K) + uint32_t(kbegin + f % kBK)) * 4u;
+    for (int i = 0; i < T::kALoads; ++i) {
+        const int f = t + i * kThreads;
+        o.a[i] = (uint32_t(min(m0 + (f >> 3), M - 1)) * uint32_t(K) + uint32_t(kbegin + ((f & 7) << 2))) * 4u;
     }
 #pragma unroll
-    for (int j = 0; j < kBK * T::kBN / kThreads; ++j) {
-        const int f = t + j * kThreads;
-        o.b[j] = (uint32_t(kbegin + f / T::kBN) * uint32_t(N) + uint32_t(min(n0 + f % T::kBN, N - 1))) * 4u;
+    for (int i = 0; i < T::kBLoads; ++i) {
+        const int f = t + i * kThreads;
+        o.b[i] = (uint32_t(kbegin + f / kRowF4) * uint32_t(N) + uint32_t(n0 + (f % kRowF4) * 4)) * 4u;
     }
 }
 
@@ -484,14 +494,41 @@ __device__ inline void buffer_offsets(int M, int N, int K, int m0, int n0, int k
 template <int TM, int TN>
 __device__ inline void load_stage_buffer(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb,
                                          const BufOffsets<TM, TN> &o, uint32_t astep, uint32_t bstep,
-                                         Regs<TM, TN> &r) {
+                                         Regs4<TM, TN> &r) {
     using T = Tile<TM, TN>;
 #pragma unroll
-    for (int j = 0; j < T::kBM * kBK / kThreads; ++j)
-        r.a[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(ra, int(o.a[j] + astep), 0, 0));
+    for (int i = 0; i < T::kALoads; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, int(o.a[i] + astep), 0, 0);
+        r.a[i] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    }
 #pragma unroll
-    for (int j = 0; j < kBK * T::kBN / kThreads; ++j)
-        r.b[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(o.b[j] + bstep), 0, 0));
+    for (int i = 0; i < T::kBLoads; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rb, int(o.b[i] + bstep), 0, 0);
+        r.b[i] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    }
+}
+
+// store_stage with k >= kend zeroed (a group's partial last stage).
+template <int TM, int TN>
+__device__ inline void store_stage4_masked(float *stage, const Regs4<TM, TN> &r, int k0, int kend, int t) {
+    using T = Tile<TM, TN>;
+    float *as = stage, *bs = stage + T::kAStage;
+#pragma unroll
+    for (int i = 0; i < T::kALoads; ++i) {
+        const int f = t + i * kThreads, kk = k0 + ((f & 7) << 2);
+        f32x4 v = r.a[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = kk + e < kend ? v[e] : 0.f;
+        *reinterpret_cast<f32x4 *>(as + (f >> 3) * kLDA + ((f & 7) << 2)) = v;
+    }
+    constexpr int kRowF4 = T::kBN / 4;
+#pragma unroll
+    for (int i = 0; i < T::kBLoads; ++i) {
+        const int f = t + i * kThreads;
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4 *>(bs + (f / kRowF4) * T::kLDB + (f % kRowF4) * 4) =
+            k0 + f / kRowF4 < kend ? r.b[i] : zero;
+    }
 }
 
 // A barrier that orders LDS only: this wave's LDS reads and writes complete
@@ -509,10 +546,11 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                                         int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
                                         int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
     using T = Tile<TM, TN>;
-    Regs<TM, TN> r[2];
+    using R = std::conditional_t<BUF, Regs4<TM, TN>, Regs<TM, TN>>;
+    R r[2];
     BufOffsets<TM, TN> off;
     __amdgpu_buffer_rsrc_t ra, rb;
-    if (BUF) {
+    if constexpr (BUF) {
         ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(A), 0, int(uint32_t(M) * uint32_t(K) * 4u),
                                                int(kBufferWord3));
         rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(B), 0, int(uint32_t(K) * uint32_t(N) * 4u),
@@ -520,17 +558,24 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
         buffer_offsets<TM, TN>(M, N, K, m0, n0, kbegin, t, off);
     }
     const uint32_t bstage = uint32_t(kBK) * uint32_t(N) * 4u;
-    auto load = [&](int s, Regs<TM, TN> &dst) {
-        if (BUF)
+    auto load = [&](int s, R &dst) {
+        if constexpr (BUF)
             load_stage_buffer<TM, TN>(ra, rb, off, uint32_t(s) * (kBK * 4u), uint32_t(s) * bstage, dst);
         else
             load_stage_clamped<TM, TN>(A, B, M, N, K, m0, n0, kbegin + s * kBK, dst, t);
     };
-    auto store = [&](float *stage, const Regs<TM, TN> &src, int k0) {
-        if (k0 + kBK <= kend)  // block-uniform
-            store_stage_plain<TM, TN>(stage, src, t);
-        else
-            store_stage_masked<TM, TN>(stage, src, k0, kend, t);
+    auto store = [&](float *stage, const R &src, int k0) {
+        if constexpr (BUF) {
+            if (k0 + kBK <= kend)  // block-uniform
+                store_stage<TM, TN>(stage, src.a, src.b, t);
+            else
+                store_stage4_masked<TM, TN>(stage, src, k0, kend, t);
+        } else {
+            if (k0 + kBK <= kend)
+                store_stage_plain<TM, TN>(stage, src, t);
+            else
+                store_stage_masked<TM, TN>(stage, src, k0, kend, t);
+        }
     };
     load(0, r[0]);
     __builtin_amdgcn_sched_barrier(0);
