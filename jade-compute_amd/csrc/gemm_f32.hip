@@ -1143,13 +1143,14 @@ constexpr int kMinGroups = 384;    // a tile shape needs ~1.5 workgroups per CU 
 constexpr int kCUs = 256;
 constexpr int kSplitTarget = 256;  // split K into about one workgroup per CU
 constexpr int kMinChunk = 128;
-// Unsplit 64x64 grids of up to one tile per CU with 16-byte rows and K of at
-// least this run four K groups (16 waves, four per SIMD) instead of two.
-// Measured on MI355X: 1024^3 22.8 -> 22.1 us, 1024x1024x2048 42.7 -> 40.5,
-// 1024x1024x4096 82.3 -> 77.4, 1000x1000x1024 25.6 -> 24.5, 768x768x1024
-// 22.6 -> 21.8; K = 512 ties (12.9 / 12.8). The unaligned loop keeps two
-// groups: with two register stages it spills at four waves per SIMD and ran
-// 15% slower (1000x777x513 18.8 -> 21.7 us).
+// Unsplit 64x64 grids of up to one tile per CU with K of at least this run
+// four K groups (16 waves, four per SIMD) instead of two. Measured on MI355X:
+// 1024^3 22.8 -> 22.1 us, 1024x1024x2048 42.7 -> 40.5, 1024x1024x4096 82.3 ->
+// 77.4, 1000x1000x1024 25.6 -> 24.5, 768x768x1024 22.6 -> 21.8; K = 512 ties
+// (12.9 / 12.8). Unaligned rows through buffer loads: 1000x777x1024 24.2 ->
+// 22.8, 1023x1000x2049 46.2 -> 44.2, but 1000x777x513 15.8 -> 16.3. The
+// clamped global-load loop (operands of 2 GiB or more) keeps two groups: it
+// spills at four waves per SIMD.
 constexpr int kFourGroupMinK = 768;
 
 // Tile choice among 128x128, 128x64 and 64x64 (128x64 measured at or above
@@ -1219,6 +1220,12 @@ void tail_tile(int tail, int &tm, int &tn) {
     tm = tn = 4 * tail <= kCUs ? 2 : 1;
 }
 
+// The unaligned loop's buffer loads address each operand with 32-bit byte
+// offsets checked against its size: both operands must be below 2 GiB.
+bool unaligned_buffers_fit(uint32_t m, uint32_t n, uint32_t k) {
+    return uint64_t(m) * k * 4 < (uint64_t(1) << 31) && uint64_t(k) * n * 4 < (uint64_t(1) << 31);
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
@@ -1262,7 +1269,8 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         }
     }
     if (p.kchunk >= 2 * kBK) p.kgroups = 2;
-    if (p.slices == 1 && k % 4 == 0 && n % 4 == 0 && p.kchunk >= kFourGroupMinK) p.kgroups = 4;
+    const bool rows16 = k % 4 == 0 && n % 4 == 0;
+    if (p.slices == 1 && p.kchunk >= kFourGroupMinK && (rows16 || unaligned_buffers_fit(m, n, k))) p.kgroups = 4;
     return p;
 }
 
@@ -1270,10 +1278,8 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
 // all are interior, aligned and within the 32-bit offsets; a per-tile choice
 // when only some are interior; register-staged otherwise.
 Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int tm, int tn, int kg) {
-    if (!vec) {  // unaligned: no tile takes the LDS-direct loads
-        const bool buffers = uint64_t(m) * k * 4 < (uint64_t(1) << 31) && uint64_t(k) * n * 4 < (uint64_t(1) << 31);
-        return buffers && tm * tn <= 2 ? kUnalignedBuf : kMixed;
-    }
+    if (!vec)  // unaligned: no tile takes the LDS-direct loads
+        return unaligned_buffers_fit(m, n, k) && tm * tn <= 2 ? kUnalignedBuf : kMixed;
     if (!dma_offsets_fit(uint32_t(64 * tm), uint32_t(64 * tn), k, n)) return kRegOnly;
     // Every K slice (the last may be shorter) must be a multiple of KG whole stages.
     const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
@@ -1297,7 +1303,7 @@ void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, co
                                int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
             break;
         case kUnalignedBuf:
-            if constexpr (TM * TN <= 2 && KG <= 2)
+            if constexpr (TM * TN <= 2)
                 hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kUnalignedBuf, KG>), grid, block, 0, stream, a, b, out,
                                    int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
             break;
@@ -1305,7 +1311,7 @@ void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, co
             if (vec)
                 hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out,
                                    int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-            else if constexpr (KG <= 2)  // four-group plans launch with two groups when unaligned
+            else if constexpr (KG <= 2)  // the clamped loop runs at most two groups
                 hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out,
                                    int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
             break;
@@ -1336,8 +1342,7 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                 uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
     }
     // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
-    // run K groups. (A four-group plan whose pointers turn out not 16-byte
-    // aligned launches with two groups.)
+    // run K groups.
     if (p.kgroups == 4)
         return {"gemm_f32_mfma_64x64x32_k4", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {4 * kThreads, 1, 1},
                 4 * Tile<1, 1>::kLdsBytes};
@@ -1454,7 +1459,10 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         return hipGetLastError();
     }
     float *out = p.slices > 1 ? workspace : c;
-    if (p.kgroups == 4 && vec) launch_tile<1, 1, 4>(stream, p, vec, a, b, out, m, n, k);
+    // A four-group plan whose loads would take the clamped global loads
+    // (pointers not 16-byte aligned, operands of 2 GiB or more) runs two groups.
+    if (p.kgroups == 4 && (vec || unaligned_buffers_fit(m, n, k)))
+        launch_tile<1, 1, 4>(stream, p, vec, a, b, out, m, n, k);
     else if (p.kgroups >= 2) launch_tile<1, 1, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
     else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);

@@ -131,7 +131,7 @@ def test_direct_tile_shapes(runtime, m, n, k, waves):
 @pytest.mark.parametrize("m,n,k,kernel", [
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # register-staged (unaligned), last group partial
-    (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows keep two groups at long K
+    (1000, 777, 700, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows, K below the four-group threshold
     (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial
     (65, 67, 63, "gemm_f32_mfma_64x64x32_k2"),  # one stage per group
     (100, 100, 40, "gemm_f32_mfma_64x64x32_k2"),  # group 1's stage lies mostly past K
@@ -156,6 +156,8 @@ def test_two_group_tile_shapes(runtime, m, n, k, kernel):
     (1000, 1000, 1024),  # edge tiles register-staged (16-byte rows), interior LDS-direct
     (1000, 600, 1000),  # 32 stages, the last partial: every tile register-staged
     (768, 768, 2048),  # 16 stages per group
+    (1000, 777, 1024),  # unaligned rows through buffer loads
+    (1023, 1000, 2049),  # unaligned rows, the last group's last stage partial
 ])
 def test_four_group_tile_shapes(runtime, m, n, k):
     # 64x64 tiles whose four K groups of four waves each sum a quarter of the

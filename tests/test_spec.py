@@ -161,9 +161,9 @@ def test_constant_bits_round_trip():
     (8192, 8192, 256, "gemm_f32_mfma_128x128x32", [4096, 1, 1]),
     (4096, 4096, 4112, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # K not a multiple of 32
     (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
-    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, aligned, K >= 768: four K groups
+    (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, K >= 768: four K groups
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2", [256, 1, 1]),  # shorter K: two K groups
-    (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),  # unaligned rows: two K groups
+    (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k4", [208, 1, 1]),  # unaligned rows through buffer loads: four too
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),
     (1536, 1024, 1024, "gemm_f32_mfma_64x64x32", [384, 1, 1]),  # 256 < tiles < 384: one group
     (512, 512, 512, "gemm_f32_direct_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K
@@ -189,7 +189,7 @@ def test_gemm_launch_plans(m, n, k, kernel, grid):
     # rounds (the rest as 128x128, 128x64 or 64x64 tiles); else the best of
     # 128x128 / 128x64 / 64x64 by round fill x tile
     # efficiency among grids of >= 384 workgroups; below that 64x64 tiles, with
-    # two K groups up to one tile per CU (four for aligned rows and K >= 768),
+    # two K groups up to one tile per CU (four for K >= 768),
     # and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
