@@ -4,20 +4,22 @@
 // ragged edges read as zero and masked on store.
 //
 // Design (gfx950, wave64):
-//  * Grids of at least 256 whole 256x256 tiles run gemm_f32_mfma_256: one
-//    512-thread workgroup per CU, eight waves of 128x64 (below); a partial last
-//    round of such tiles runs as 128x128, 128x64 or 64x64 tiles of the kernel
-//    below.
-//  * Otherwise a 256-thread workgroup is a 2x2 grid of waves; each wave owns
-//    TM x TN blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per
-//    block), so a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64 or
-//    64x64. Two independent products of one shape can share a launch. Grids
-//    of at most one 64x64 tile per CU run two such groups of four waves per
-//    workgroup (KG = 2), each over half of the tile's K stages.
+//  * A 256-thread workgroup is a 2x2 grid of waves; each wave owns TM x TN
+//    blocks of v_mfma_f32_32x32x2_f32 (16 accumulators per lane per block), so
+//    a workgroup tile is (64*TM) x (64*TN): 128x128, 128x64 or 64x64, two
+//    workgroups per CU. Two independent products of one shape can share a
+//    launch. Grids of at most one 64x64 tile per CU run two or four such
+//    groups of four waves per workgroup (KG), each over a share of the tile's
+//    K stages.
+//  * Grids of at least 256 whole 256x256 tiles run as 128x128 tiles, or, when
+//    that grid's last round would be under a quarter full, as whole rounds of
+//    gemm_f32_mfma_256 (one 512-thread workgroup per CU, eight waves of
+//    128x64) plus a partial round of 128x128 or 64x64 tiles.
 //  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
 //    LDS-direct loads (interior tiles) or a register prefetch (edge tiles and
 //    unaligned shapes; unaligned 64x64 and 128x64 tiles keep two stages in
-//    registers), with one barrier per stage.
+//    registers, loaded through buffer instructions), with one barrier per
+//    stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
@@ -26,11 +28,11 @@
 //  * Workgroup ids are remapped so each of the 8 XCDs (dispatched round-robin)
 //    owns a contiguous range of tiles in grouped order, keeping A rows and B
 //    columns hot in that XCD's private L2.
-//  * Two-level accumulation: each 32-deep K stage is summed by the matrix
-//    cores into zeroed accumulators and then added to the running sums with
-//    round-to-nearest VALU adds. A single chained MFMA accumulation over
-//    K = 4096 drifted by ~3.6e-4 absolute on unit-scale inputs, outside the
-//    1e-4 gate; the stage split keeps the long recurrence to K/32 adds.
+//  * Two-level accumulation: a run of one or two 32-deep K stages is summed by
+//    the matrix cores into zeroed accumulators and then added to the running
+//    sums with round-to-nearest VALU adds. A single chained MFMA accumulation
+//    over K = 4096 drifted by ~3.6e-4 absolute on unit-scale inputs, outside
+//    the 1e-4 gate; the split keeps the long recurrence to K/32 or K/64 adds.
 //  * Small grids with aligned A rows and moderate K run gemm_f32_direct: 32x32
 //    tiles whose waves split K, operands loaded straight into registers, one
 //    launch (below).
