@@ -1228,6 +1228,41 @@ bool unaligned_buffers_fit(uint32_t m, uint32_t n, uint32_t k) {
     return uint64_t(m) * k * 4 < (uint64_t(1) << 31) && uint64_t(k) * n * 4 < (uint64_t(1) << 31);
 }
 
+// A second look at grids of more than one 64x64 tile per CU, over the tile
+// shapes (index into {128x128, 128x64, 64x64}) whose grid has no edge tile.
+// Such a grid runs every tile on the LDS-direct loop; one edge tile puts the
+// whole launch on the mixed-path kernel. Its cost is the busiest CU's work:
+// ceil(tiles / 256) tiles x tile area / the tile's efficiency (1.00 / 0.97 /
+// 0.87; 0.93 / 0.90 for 128x128 / 128x64 grids of at most one tile per CU,
+// which run one wave per SIMD). The edge-free choice replaces the round-fill
+// choice `old` when `old` has edge tiles, or when it is predicted at least 5%
+// faster, except that K below 512 keeps the smaller tile. Measured on MI355X
+// (TFLOP/s, round-fill -> edge-free): 3072x1024x4096 98.9 -> 113.4 (128x64 ->
+// 64x64), 2048x1536x512 87.5 -> 100.4, 2048x3072x1024 114.1 -> 122.8 (64x64 ->
+// 128x64), 6144x1024x1024 114.6 -> 123.5, 2304^3 100.4 -> 108.0, 3648^2x1024
+// 102.3 -> 112.6 (128x128 with edge tiles -> 64x64); at K = 384 the larger
+// tile lost (2048x3072x384 103.3 -> 92.5), and predicted gains under 5% were
+// ties or losses (12288x1024x1024 128x64 127.5, 128x128 122.8).
+int edge_free_choice(uint32_t m, uint32_t n, uint32_t k, int old) {
+    const int shapes[3][2] = {{2, 2}, {2, 1}, {1, 1}};
+    const double eff_shared[3] = {1.00, 0.97, 0.87}, eff_alone[3] = {0.93, 0.90, 0.87};
+    auto edge_free = [&](int i) { return m % (64u * shapes[i][0]) == 0 && n % (64u * shapes[i][1]) == 0; };
+    auto cost = [&](int i) {
+        const uint64_t tiles = uint64_t((m + 64 * shapes[i][0] - 1) / (64 * shapes[i][0])) *
+                               ((n + 64 * shapes[i][1] - 1) / (64 * shapes[i][1]));
+        const double per_cu = double((tiles + kCUs - 1) / kCUs), area = shapes[i][0] * shapes[i][1];
+        return per_cu * area / (tiles > uint64_t(kCUs) ? eff_shared[i] : eff_alone[i]);
+    };
+    int cand = -1;
+    for (int i = 0; i < 3; ++i)
+        if (edge_free(i) && (cand < 0 || cost(i) < cost(cand))) cand = i;
+    if (cand < 0 || cand == old) return old;
+    if (!edge_free(old)) return cand;
+    const bool larger = shapes[cand][0] * shapes[cand][1] > shapes[old][0] * shapes[old][1];
+    if (larger && k < 512) return old;
+    return cost(old) > 1.05 * cost(cand) ? cand : old;
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
@@ -1254,10 +1289,12 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const double score = eff[i] * double(groups) / double(kSlots * rounds);
         if (score > best_score) best = i, best_score = score;
     }
-    if (best >= 0) return grid(shapes[best][0], shapes[best][1]);
     Plan p = grid(1, 1);
     const int t = p.tiles_m * p.tiles_n;
-    if (t > kCUs) return p;
+    if (t > kCUs) {
+        const int pick = edge_free_choice(m, n, k, best >= 0 ? best : 2);
+        return grid(shapes[pick][0], shapes[pick][1]);
+    }
     if (t <= kCUs / 2) {
         if (const int g = direct_waves(m, n, k))
             return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1, 0, 0};

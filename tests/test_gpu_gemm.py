@@ -191,6 +191,23 @@ def test_large_grid_shapes(runtime, m, n, k, want):
     gate(got, m, n, k, a, b)
 
 
+@pytest.mark.parametrize("m,n,k,want", [
+    (2048, 1536, 512, "gemm_f32_mfma_64x64x32"),  # round fill picked 128x64; three 64x64 tiles per CU
+    (1024, 6144, 512, "gemm_f32_mfma_128x64x32"),  # round fill picked 64x64; K >= 512 takes the larger tile
+    (1088, 1088, 512, "gemm_f32_mfma_64x64x32"),  # 128x64 would leave edge tiles
+])
+def test_edge_free_plan_shapes(runtime, m, n, k, want):
+    # Grids of more than one 64x64 tile per CU whose plan the edge-free
+    # second look changes, or would change but for its limits.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == want, kernel.launch
+    a = orc.values(m * k, 0x7A, 1.0)
+    b = orc.values(k * n, 0x8B, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b, rows=(0, 256))
+    gate(got, m, n, k, a, b, rows=(m - 256, m))
+
+
 # A seeded sample (random.Random(20261201)) of shapes below 2e8 products,
 # drawn so that every small- and mid-grid plan family appears: direct-load
 # 32x32 tiles, 64x64 tiles with two K groups (whole or split K), 64x64,

@@ -83,7 +83,7 @@ def test_fused_gate_up_swiglu_is_bit_identical(runtime):
     # gemm(x, Wg -> G), gemm(x, Wu -> U), swi_glu(G, U -> D) on whole 128x64
     # tiles run as one fused launch; each of G, U and D must equal the three
     # jobs launched one at a time, bit for bit.
-    m, n, k = 1024, 3072, 256
+    m, n, k = 2048, 2048, 256
     specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "swiglu": {"op": "swi_glu", "len": m * n}}
     assert "128x64" in runtime.compile(specs["gemm"]).launch["kernel"]
     arrays = {"x": orc.normal(m * k, 0x21), "wg": orc.normal(k * n, 0x22, 0.0, 0.1),
@@ -105,9 +105,11 @@ def test_swiglu_writing_a_gemm_input_is_not_fused(runtime):
     # swi_glu writes the gate weights the GEMMs read (k == m so the lengths
     # match): fusing would overwrite Wg while other workgroups still read it,
     # so the batch keeps its order; two repeats make the second read the
-    # overwritten weights.
-    m, n, k = 1024, 3072, 1024
+    # overwritten weights. The shape plans whole 128x64 tiles, so only the
+    # hazard keeps the jobs apart.
+    m, n, k = 2048, 2048, 2048
     specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "swiglu": {"op": "swi_glu", "len": m * n}}
+    assert "128x64" in runtime.compile(specs["gemm"]).launch["kernel"]
     arrays = {"x": orc.normal(m * k, 0x31, 0.0, 0.05), "wg": orc.normal(k * n, 0x32, 0.0, 0.05),
               "wu": orc.normal(k * n, 0x33, 0.0, 0.05), "g": m * n, "u": m * n}
     plan = [("gemm", ["x", "wg", "g"]), ("gemm", ["x", "wu", "u"]), ("swiglu", ["g", "u", "wg"])]

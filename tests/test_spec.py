@@ -180,7 +180,12 @@ def test_constant_bits_round_trip():
     (3072, 3072, 3072, "gemm_f32_mfma_64x64x32", [2304, 1, 1]),  # 128x128 would fill 56% of two rounds
     (2500, 2500, 2500, "gemm_f32_mfma_128x128x32", [400, 1, 1]),
     (1024, 4096, 4096, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # 128x64 also for wide C
-    (6144, 1024, 1024, "gemm_f32_mfma_64x64x32", [1536, 1, 1]),
+    (6144, 1024, 1024, "gemm_f32_mfma_128x64x32", [768, 1, 1]),  # edge-free, 3 tiles per CU against 6 half-size
+    (2048, 3072, 1024, "gemm_f32_mfma_128x64x32", [768, 1, 1]),
+    (2048, 3072, 384, "gemm_f32_mfma_64x64x32", [1536, 1, 1]),  # K < 512 keeps the smaller tile
+    (3072, 1024, 4096, "gemm_f32_mfma_64x64x32", [768, 1, 1]),  # 3 tiles per CU against 2 of twice the size
+    (3648, 3648, 1024, "gemm_f32_mfma_64x64x32", [3249, 1, 1]),  # 128x128 would leave edge tiles
+    (12288, 1024, 1024, "gemm_f32_mfma_128x64x32", [1536, 1, 1]),  # 128x128 predicted < 5% faster: kept
     (4096, 2816, 1024, "gemm_f32_mfma_128x64x32", [1408, 1, 1]),  # MLP gate/up
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
@@ -188,8 +193,11 @@ def test_gemm_launch_plans(m, n, k, kernel, grid):
     # last round would be under a quarter full: then 256x256 for the whole
     # rounds (the rest as 128x128, 128x64 or 64x64 tiles); else the best of
     # 128x128 / 128x64 / 64x64 by round fill x tile
-    # efficiency among grids of >= 384 workgroups; below that 64x64 tiles, with
-    # two K groups up to one tile per CU (four for K >= 768),
+    # efficiency among grids of >= 384 workgroups, replaced by the edge-free
+    # tile whose busiest CU finishes first when that choice has edge tiles or
+    # is predicted 5% slower (K < 512 keeps the smaller tile); with at most
+    # one 64x64 tile per CU, 64x64 tiles with
+    # two K groups (four for K >= 768),
     # and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
