@@ -81,18 +81,24 @@ void or_dot(size_t m, size_t n, size_t k, const double *a, const double *b,
     }
 }
 
-void or_attention_reference(uint32_t heads, uint32_t seq, uint32_t dim,
+int or_attention_reference(uint32_t heads, uint32_t seq, uint32_t dim,
                             int causal, const float *q, const float *k,
                             const float *v, double *out, uint32_t row0,
                             uint32_t row1, int threads) {
     const size_t rows_per_head = (size_t)(row1 - row0);
     const long total = (long)((size_t)heads * rows_per_head);
     const double root = sqrt((double)dim);
+    int failed = 0;
 #pragma omp parallel num_threads(clamp_threads(threads))
     {
         double *scores = (double *)malloc(sizeof(double) * (seq ? seq : 1));
+        if (!scores) {
+#pragma omp atomic write
+            failed = 1;
+        }
 #pragma omp for schedule(dynamic, 1)
         for (long item = 0; item < total; ++item) {
+            if (!scores) continue;
             const size_t h = (size_t)item / rows_per_head;
             const size_t row = row0 + (size_t)item % rows_per_head;
             const size_t count = causal ? row + 1 : seq;
@@ -120,6 +126,7 @@ void or_attention_reference(uint32_t heads, uint32_t seq, uint32_t dim,
         }
         free(scores);
     }
+    return failed;
 }
 
 double or_sigmoid(double x) {
@@ -162,12 +169,12 @@ void or_swiglu(size_t len, const float *gate, const float *up, double *out) {
     }
 }
 
-void or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
-            const float *norm, const float *wg, const float *wu,
-            const float *wd, double eps, double *out, int threads) {
+int or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
+           const float *norm, const float *wg, const float *wu,
+           const float *wd, double eps, double *out, int threads) {
     const size_t xw = batch * width, wh = width * hidden, bh = batch * hidden;
     double *xd = (double *)malloc(sizeof(double) * xw);
-    double *nd = (double *)malloc(sizeof(double) * width);
+    double *nd = (double *)calloc(width ? width : 1, sizeof(double));
     double *wgd = (double *)malloc(sizeof(double) * wh);
     double *wud = (double *)malloc(sizeof(double) * wh);
     double *wdd = (double *)malloc(sizeof(double) * wh);
@@ -175,6 +182,11 @@ void or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
     double *gate = (double *)malloc(sizeof(double) * bh);
     double *upv = (double *)malloc(sizeof(double) * bh);
     double *proj = (double *)malloc(sizeof(double) * xw);
+    if (!xd || !nd || !wgd || !wud || !wdd || !normalized || !gate || !upv || !proj) {
+        free(xd); free(nd); free(wgd); free(wud); free(wdd);
+        free(normalized); free(gate); free(upv); free(proj);
+        return 1;
+    }
     for (size_t i = 0; i < xw; ++i) xd[i] = (double)x[i];
     for (size_t i = 0; i < width; ++i) nd[i] = (double)norm[i];
     for (size_t i = 0; i < wh; ++i) {
@@ -190,6 +202,7 @@ void or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
     for (size_t i = 0; i < xw; ++i) out[i] = proj[i] + (double)x[i];
     free(xd); free(nd); free(wgd); free(wud); free(wdd);
     free(normalized); free(gate); free(upv); free(proj);
+    return 0;
 }
 
 void or_compare(const float *actual, const double *expected, size_t len,

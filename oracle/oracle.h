@@ -51,8 +51,9 @@ void or_dot(size_t m, size_t n, size_t k, const double *a, const double *b,
 
 /* metal_lab::attention_reference, src/runtime/metal_lab.rs:33-73:
  * materialised FP64 rows, score = sum_d q*k / sqrt(dim), max-subtracted exp,
- * out = sum_col p/denom * v. Query rows [row0, row1) of every head. */
-void or_attention_reference(uint32_t heads, uint32_t seq, uint32_t dim,
+ * out = sum_col p/denom * v. Query rows [row0, row1) of every head.
+ * Returns 0, or 1 when a thread's score buffer cannot be allocated. */
+int or_attention_reference(uint32_t heads, uint32_t seq, uint32_t dim,
                             int causal, const float *q, const float *k,
                             const float *v, double *out, uint32_t row0,
                             uint32_t row1, int threads);
@@ -72,10 +73,11 @@ void or_softmax(size_t rows, size_t cols, const float *x, double *out,
 /* SwiGLU expectation, src/runtime/workloads.rs:96-100: g * sigmoid(g) * u. */
 void or_swiglu(size_t len, const float *gate, const float *up, double *out);
 
-/* Residual MLP chain, src/runtime/workloads.rs:466-479 (FP64 throughout). */
-void or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
-            const float *norm, const float *wg, const float *wu,
-            const float *wd, double eps, double *out, int threads);
+/* Residual MLP chain, src/runtime/workloads.rs:466-479 (FP64 throughout).
+ * Returns 0, or 1 when the FP64 intermediates cannot be allocated. */
+int or_mlp(size_t batch, size_t width, size_t hidden, const float *x,
+           const float *norm, const float *wg, const float *wu,
+           const float *wd, double eps, double *out, int threads);
 
 /* workloads::compare, src/runtime/workloads.rs:224-243. */
 typedef struct or_check {

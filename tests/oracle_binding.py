@@ -38,12 +38,14 @@ def _load():
     lib.or_normal.argtypes = [_vp, sz, u32, f32, f32]
     lib.or_gemm_reference.argtypes = [u32, u32, u32, _vp, _vp, _vp, u32, u32, i32]
     lib.or_dot.argtypes = [sz, sz, sz, _vp, _vp, _vp, i32]
+    lib.or_attention_reference.restype = i32
     lib.or_attention_reference.argtypes = [u32, u32, u32, i32, _vp, _vp, _vp, _vp, u32, u32, i32]
     lib.or_sigmoid.restype = f64
     lib.or_sigmoid.argtypes = [f64]
     lib.or_normalize.argtypes = [sz, sz, _vp, _vp, f64, _vp, i32]
     lib.or_softmax.argtypes = [sz, sz, _vp, _vp, i32]
     lib.or_swiglu.argtypes = [sz, _vp, _vp, _vp]
+    lib.or_mlp.restype = i32
     lib.or_mlp.argtypes = [sz, sz, sz, _vp, _vp, _vp, _vp, _vp, f64, _vp, i32]
     lib.or_compare.argtypes = [_vp, _vp, sz, f64, f64, _c.POINTER(Check)]
     lib.or_check_gemm.argtypes = [u32, u32, u32, _vp, _vp, _vp, sz, i32, _c.POINTER(Validation)]
@@ -111,7 +113,9 @@ def attention_reference(heads, seq, dim, causal, q, k, v, rows=None, threads=THR
     q, k, v = _f32(q), _f32(k), _f32(v)
     r0, r1 = (0, seq) if rows is None else rows
     out = np.empty(heads * (r1 - r0) * dim, np.float64)
-    lib.or_attention_reference(heads, seq, dim, 1 if causal else 0, _p(q), _p(k), _p(v), _p(out), r0, r1, threads)
+    if lib.or_attention_reference(heads, seq, dim, 1 if causal else 0, _p(q), _p(k), _p(v), _p(out), r0, r1,
+                                  threads):
+        raise MemoryError("or_attention_reference: score buffer allocation failed")
     return out
 
 
@@ -143,7 +147,8 @@ def swiglu(gate, up):
 def mlp(batch, width, hidden, x, norm, wg, wu, wd, eps, threads=THREADS):
     x, norm, wg, wu, wd = (_f32(t) for t in (x, norm, wg, wu, wd))
     out = np.empty(batch * width, np.float64)
-    lib.or_mlp(batch, width, hidden, _p(x), _p(norm), _p(wg), _p(wu), _p(wd), eps, _p(out), threads)
+    if lib.or_mlp(batch, width, hidden, _p(x), _p(norm), _p(wg), _p(wu), _p(wd), eps, _p(out), threads):
+        raise MemoryError("or_mlp: FP64 intermediate allocation failed")
     return out
 
 
