@@ -1013,9 +1013,9 @@ struct Slice {
 
 // A 4-float run clamped to start at most at K - 4 stays inside its row.
 __device__ inline void load_slice(const float *__restrict__ A, const float *__restrict__ B, int K, int N,
-                                  size_t arow, int bcol, int k0, int h, Slice &s) {
+                                  size_t arow, int lda, int bcol, int k0, int h, Slice &s) {
     const int kb = k0 + 16 * h;
-    const float *ap = A + arow * K;
+    const float *ap = A + arow * lda;
 #pragma unroll
     for (int q = 0; q < 4; ++q) s.a[q] = *reinterpret_cast<const f32x4 *>(ap + min(kb + 4 * q, K - 4));
 #pragma unroll
@@ -1040,11 +1040,12 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 }  // namespace direct
 
 // gridDim.y > 1: a batch of independent products, product z at A + z*sa,
-// B + z*sb, C + z*sc (attention's P.V per head).
+// B + z*sb, C + z*sc (attention's P.V per head, or the K slices of a split
+// product: sa = K, sb = K*N with A rows lda apart).
 template <int G>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
-                                                          float *__restrict__ C, int M, int N, int K, int tiles_m,
-                                                          int tiles_n, size_t sa = 0, size_t sb = 0,
+                                                          float *__restrict__ C, int M, int N, int K, int lda,
+                                                          int tiles_m, int tiles_n, size_t sa = 0, size_t sb = 0,
                                                           size_t sc = 0) {
     using namespace direct;
     constexpr int D = kDepth;
@@ -1073,7 +1074,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
     if (count > 0) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            load_slice(A, B, K, N, arow, bcol, slice_k(d), h, buf[d]);
+            load_slice(A, B, K, N, arow, lda, bcol, slice_k(d), h, buf[d]);
             __builtin_amdgcn_sched_barrier(0);  // loads issued slice by slice
         }
         int i = 0;
@@ -1081,7 +1082,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 mma_slice(buf[d], valid(i + d), acc);
-                load_slice(A, B, K, N, arow, bcol, slice_k(i + d + D), h, buf[d]);
+                load_slice(A, B, K, N, arow, lda, bcol, slice_k(i + d + D), h, buf[d]);
                 // Keep the slices in order: interleaving their independent
                 // MFMA chains would make the first one wait for every load.
                 __builtin_amdgcn_sched_barrier(0);
@@ -1210,6 +1211,28 @@ int direct_waves(uint32_t m, uint32_t n, uint32_t k) {
     return g;
 }
 
+// Products of at most 32 rows (one 32-row tile: decode-like shapes) that the
+// unsplit direct plan does not take stream B through direct-load 32x32 tiles
+// split over K: four waves per tile, the K slices a batch of products into the
+// workspace, summed in slice order by the reduce. The slice count aims at
+// ~1536 waves, divides K into runs of a multiple of 4 (one run length for the
+// batch) of at least 128, and needs at least 1024 waves. Measured on MI355X
+// against the 64x64 split or
+// K-group tiles: 1x4096x4096 27.4 -> 20.4 us, 1x11008x4096 79.5 -> 45.7,
+// 32x11008x4096 79.7 -> 48.3, 16x1024x2816 13.2 -> 11.6. From 64 rows the
+// 32x32 tiles read B once per 32 rows and lose (64x4096x4096 28.1 -> 34.2).
+// Returns the slice count, or 0 where the plan does not apply.
+int skinny_slices(uint32_t m, uint32_t n, uint32_t k) {
+    if (m > 32 || k % 4 != 0 || k < 128) return 0;
+    const uint64_t t64 = uint64_t((n + 63) / 64);
+    if (t64 > uint64_t(kCUs)) return 0;
+    const uint32_t tiles = (n + 31) / 32;
+    int s = int(std::min<uint32_t>(16, (1536 + 4 * tiles - 1) / (4 * tiles)));
+    while (s > 1 && (k % uint32_t(s) != 0 || (k / uint32_t(s)) % 4 != 0 || k / uint32_t(s) < 128)) --s;
+    // Below ~1024 waves the streams fall short (1x4096x4096 unsplit: 31.7 us).
+    return uint64_t(tiles) * uint64_t(s) * 4 >= 1024 ? s : 0;
+}
+
 // The partial last round of a 256x256 grid (`tail` such tiles) runs as
 // 128x128 tiles when those are at most one workgroup per CU, else as 64x64
 // tiles. Measured with the whole rounds before it: 5120x5120x2048 (144 tail
@@ -1295,9 +1318,12 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const int pick = edge_free_choice(m, n, k, best >= 0 ? best : 2);
         return grid(shapes[pick][0], shapes[pick][1]);
     }
-    if (t <= kCUs / 2) {
+    if (t <= kCUs / 2)
         if (const int g = direct_waves(m, n, k))
             return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1, 0, 0};
+    if (const int s = skinny_slices(m, n, k))
+        return {1, 1, s, int(k / s), 1, int((n + 31) / 32), false, 0, 4, 1, 0, 0};
+    if (t <= kCUs / 2) {
         const int want = (kSplitTarget + t - 1) / t;
         const int most = int(k / kMinChunk);
         p.slices = std::max(1, std::min(want, most));
@@ -1375,8 +1401,8 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     if (p.direct) {
         static const char *names[3] = {"gemm_f32_direct_32x32x32_w1", "gemm_f32_direct_32x32x32_w2",
                                        "gemm_f32_direct_32x32x32_w4"};
-        return {names[p.direct == 4 ? 2 : p.direct - 1],
-                {uint32_t(p.tiles_m * p.tiles_n), 1, 1},
+        return {p.slices > 1 ? "gemm_f32_direct_32x32x32_w4_splitk" : names[p.direct == 4 ? 2 : p.direct - 1],
+                {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {uint32_t(64 * p.direct), 1, 1},
                 uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
     }
@@ -1446,7 +1472,7 @@ hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const flo
     if (k % 4 != 0 || ((reinterpret_cast<uintptr_t>(a) | sa * sizeof(float)) & 15u) != 0) return hipErrorInvalidValue;
     const int tiles_m = int((m + 31) / 32), tiles_n = int((n + 31) / 32);
     const dim3 grid(unsigned(tiles_m * tiles_n), batch), block(256);
-    hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), tiles_m, tiles_n, sa,
+    hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k), tiles_m, tiles_n, sa,
                        sb, sc);
     return hipGetLastError();
 }
@@ -1482,18 +1508,30 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
     if (p.direct) {
         const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
         if ((reinterpret_cast<uintptr_t>(a) & 15u) != 0) {
-            // Unaligned A: the 64x64 register-staged tiles (no split, no workspace).
-            const Plan q{1, 1, 1, p.kchunk, int((m + 63) / 64), int((n + 63) / 64), false, 0, 0, 1, 0, 0};
+            // Unaligned A: the 64x64 register-staged tiles (no split).
+            const Plan q{1, 1, 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 63) / 64), int((n + 63) / 64), false, 0, 0,
+                         1, 0, 0};
             launch_tile<1, 1>(stream, q, false, a, b, c, m, n, k);
+        } else if (p.slices > 1) {
+            // K slices of p.kchunk (which divides K) as a batch of products
+            // into the workspace, then the ordered reduce.
+            const size_t mn = size_t(m) * n;
+            hipLaunchKernelGGL(gemm_f32_direct<4>, dim3(grid.x, unsigned(p.slices)), block, 0, stream, a, b, workspace,
+                               int(m), int(n), p.kchunk, int(k), p.tiles_m, p.tiles_n, size_t(p.kchunk),
+                               size_t(p.kchunk) * n, mn);
+            const hipError_t status = hipGetLastError();
+            if (status != hipSuccess) return status;
+            hipLaunchKernelGGL(splitk_reduce, dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, stream, workspace, c, mn,
+                               p.slices);
         } else if (p.direct == 4) {
-            hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
-                               p.tiles_n);
+            hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
+                               p.tiles_m, p.tiles_n);
         } else if (p.direct == 2) {
-            hipLaunchKernelGGL(gemm_f32_direct<2>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
-                               p.tiles_n);
+            hipLaunchKernelGGL(gemm_f32_direct<2>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
+                               p.tiles_m, p.tiles_n);
         } else {
-            hipLaunchKernelGGL(gemm_f32_direct<1>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), p.tiles_m,
-                               p.tiles_n);
+            hipLaunchKernelGGL(gemm_f32_direct<1>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
+                               p.tiles_m, p.tiles_n);
         }
         return hipGetLastError();
     }

@@ -137,7 +137,7 @@ def test_direct_tile_shapes(runtime, m, n, k, waves):
     (100, 100, 40, "gemm_f32_mfma_64x64x32_k2"),  # group 1's stage lies mostly past K
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2"),
     (200, 8, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),  # ragged last slice
-    (1, 1024, 4096, "gemm_f32_mfma_64x64x32_splitk_k2"),
+    (40, 1024, 4096, "gemm_f32_mfma_64x64x32_splitk_k2"),  # over 32 rows: not the skinny plan
 ])
 def test_two_group_tile_shapes(runtime, m, n, k, kernel):
     # 64x64 tiles whose two K groups of four waves sum the two halves of each
@@ -188,6 +188,25 @@ def test_large_grid_shapes(runtime, m, n, k, want):
     a = orc.values(m * k, 0x77, 1.0)
     b = orc.values(k * n, 0x88, 1.0)
     got = run_gemm(runtime, m, n, k, a, b)
+    gate(got, m, n, k, a, b)
+
+
+@pytest.mark.parametrize("m,n,k,slices", [
+    (1, 4096, 4096, 2),  # a single row
+    (16, 1024, 2816, 11),  # 11 runs of 256
+    (31, 3000, 1000, 5),  # ragged N and M, runs of 200
+    (32, 8192, 2048, 2),
+    (1, 1024, 4096, 8),
+])
+def test_skinny_direct_split_shapes(runtime, m, n, k, slices):
+    # At most 32 rows: direct-load 32x32 tiles split over K into a batch of
+    # products (A rows K apart), summed in slice order by the reduce.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == "gemm_f32_direct_32x32x32_w4_splitk", kernel.launch
+    assert kernel.launch["grid"][1] == slices, kernel.launch
+    a = orc.values(m * k, 0x5C, 1.0)
+    b = orc.values(k * n, 0x6D, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
     gate(got, m, n, k, a, b)
 
 

@@ -170,6 +170,11 @@ def test_constant_bits_round_trip():
     (700, 700, 700, "gemm_f32_direct_32x32x32_w4", [484, 1, 1]),  # 6 slices per wave
     (768, 768, 768, "gemm_f32_mfma_64x64x32_k4", [144, 1, 1]),  # > 128 64x64 tiles: not direct
     (255, 257, 4, "gemm_f32_direct_32x32x32_w1", [72, 1, 1]),  # one slice: one wave
+    (1, 4096, 4096, "gemm_f32_direct_32x32x32_w4_splitk", [128, 2, 1]),  # <= 32 rows: K split ~1536 waves
+    (16, 1024, 2816, "gemm_f32_direct_32x32x32_w4_splitk", [32, 11, 1]),  # slices divide K
+    (1, 16384, 4096, "gemm_f32_direct_32x32x32_w4", [512, 1, 1]),  # enough tiles unsplit
+    (1, 4096, 4100, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),  # no divisor of K gives 1024 waves
+    (33, 4096, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),  # over 32 rows
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2", [128, 2, 1]),  # 8 slices per wave: split K
     (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),
     (256, 256, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [16, 16, 1]),
@@ -196,7 +201,8 @@ def test_gemm_launch_plans(m, n, k, kernel, grid):
     # efficiency among grids of >= 384 workgroups, replaced by the edge-free
     # tile whose busiest CU finishes first when that choice has edge tiles or
     # is predicted 5% slower (K < 512 keeps the smaller tile); with at most
-    # one 64x64 tile per CU, 64x64 tiles with
+    # one 64x64 tile per CU, products of at most 32 rows as direct-load 32x32
+    # tiles split over K, else 64x64 tiles with
     # two K groups (four for K >= 768),
     # and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
