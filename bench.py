@@ -4,15 +4,20 @@ A step is one pass of the hot path over one batch of synthetic input. The
 headline step (`value`) is the FP32 GEMM C = A.B at 4096^3 from BASELINE
 configs[1], inputs from validation::inputs (xorshift32 seeds 0x12345678 /
 0x9abcdef1, U[-1,1)), resident in HBM before timing. The same JSON line
-carries the causal attention config (B4 H32 S4096 D128), the Softmax
-32768x4096 bandwidth case, the six-op MLP block and the rest of the GEMM
-sweep.
+carries the causal attention config (B4 H32 S4096 D128), attention C3, the
+Softmax 32768x4096 bandwidth case, the six-op MLP block, the rest of the GEMM
+sweep and the copy calibration.
 
-Timing follows the reference's jr_execute scope (native/jade_runtime_corex.cpp:
-148-189): W untimed replays, then hipEvents around K ordered launches on the
-runtime's stream (the stream every kernel runs on). `roofline.achieved` is the
-dominant kernel's algorithmic FLOP per launch divided by the event-measured
-average launch time.
+Timing follows the reference's harness (src/runtime/metal_lab.rs:75-107,
+179-187): each workload gets W untimed warm-up steps and a time-based
+pre-heat (--preheat-ms of device time, reported as `preheat_ms`), then its K
+timed steps run as nine samples, interleaved with the other headline workload
+in rotating order, each sample timed by hipEvents around its launches on the
+runtime's stream (the jr_execute scope, native/jade_runtime_corex.cpp:
+148-189). The reported per-step time is the median sample; the mean and the
+extremes are listed beside it. Bandwidth-bound ops are rotated over copies of
+their buffers that exceed the 256 MB MALL three times, so their GB/s are HBM
+figures.
 
 The CPU baseline is the reference's own CPU path, its FP64 oracle loops
 (restated in oracle/), timed on this host on a bounded sample; those sampled
@@ -42,15 +47,81 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def timed(rt, jobs, steps, warmup):
-    if warmup:
-        rt.execute(jobs, warmup)
-    started = time.perf_counter()
-    ex = rt.execute(jobs, steps)
-    wall_ms = (time.perf_counter() - started) * 1000.0
-    if ex.gpu_ms is None:
-        raise RuntimeError("device timer returned no duration")
-    return ex.gpu_ms / steps, wall_ms / steps
+# The reference's harness method (src/runtime/metal_lab.rs:75-107,179-187;
+# reports/METAL_ADVANCES.md:109-120): warm up, then interleaved samples,
+# report the median per-step time. Here every workload also gets a time-based
+# pre-heat before its samples: the MI355X clock ramps over the first ~30 ms of
+# sustained matrix work, which a fixed warm-up count does not cover for short
+# launches.
+SAMPLES = 9
+PREHEAT_MS = 100.0
+MALL_BYTES = 256 << 20  # last-level (Infinity) cache in front of HBM
+
+
+def split_steps(steps, samples=SAMPLES):
+    """`steps` timed steps as at most `samples` samples (sizes differ by <= 1)."""
+    count = max(1, min(samples, steps))
+    base, extra = divmod(steps, count)
+    return [base + (1 if i < extra else 0) for i in range(count)]
+
+
+def median(values):
+    v = sorted(values)
+    n = len(v)
+    return v[n // 2] if n % 2 else 0.5 * (v[n // 2 - 1] + v[n // 2])
+
+
+class Workload:
+    """One batch of jobs on the runtime; a step is one replay of the batch
+    (`launches` kernel launches of the op being measured)."""
+
+    def __init__(self, rt, jobs, launches=1):
+        self.rt, self.jobs, self.launches = rt, jobs, launches
+        self.preheat_ms = 0.0
+        self.samples, self.sizes, self.host = [], [], []
+
+    def warm(self, warmup):
+        if warmup:
+            self.rt.execute(self.jobs, warmup)
+
+    def preheat(self, target_ms=PREHEAT_MS):
+        batch = 1
+        while self.preheat_ms < target_ms:
+            ex = self.rt.execute(self.jobs, batch)
+            self.preheat_ms += ex.gpu_ms or 0.0
+            batch = min(2 * batch, 1 << 14)
+
+    def sample(self, steps):
+        ex = self.rt.execute(self.jobs, steps)
+        if ex.gpu_ms is None:
+            raise RuntimeError("device timer returned no duration")
+        self.samples.append(ex.gpu_ms / steps)
+        self.host.append(ex.host_ms / steps)
+        self.sizes.append(steps)
+
+    def summary(self):
+        """Per-step times in ms: median of the samples (the reported figure),
+        mean over all timed steps, extremes, and per-launch median."""
+        total = sum(s * n for s, n in zip(self.samples, self.sizes))
+        return {"ms_per_step": median(self.samples), "mean_ms_per_step": total / sum(self.sizes),
+                "min_ms_per_step": min(self.samples), "max_ms_per_step": max(self.samples),
+                "wall_ms_per_step": median(self.host), "samples": len(self.samples), "timed_steps": sum(self.sizes),
+                "sample_steps": list(self.sizes), "samples_ms_per_step": [round(s, 6) for s in self.samples],
+                "preheat_ms": self.preheat_ms, "ms_per_launch": median(self.samples) / self.launches}
+
+
+def measure(workloads, steps, warmup):
+    """Warm-up, pre-heat, then `steps` timed steps of each workload as
+    interleaved samples: sample round r runs the workloads in an order rotated
+    by r (metal_lab.rs:179-187). Returns {name: summary}."""
+    names = list(workloads)
+    for name in names:
+        workloads[name].warm(warmup)
+        workloads[name].preheat()
+    for r, size in enumerate(split_steps(steps)):
+        for off in range(len(names)):
+            workloads[names[(r + off) % len(names)]].sample(size)
+    return {name: workloads[name].summary() for name in names}
 
 
 def traffic_from_profiles(symbol_prefix, launch):
@@ -71,7 +142,20 @@ def traffic_from_profiles(symbol_prefix, launch):
     return None
 
 
-def bench_gemm(rt, m, n, k, steps, warmup, keep=False):
+class Prepared:
+    """Device buffers and jobs of one workload, freed by close()."""
+
+    def __init__(self, rt, jobs, buffers, info, launches=1):
+        self.workload = Workload(rt, jobs, launches)
+        self.buffers, self.info = buffers, info
+
+    def close(self):
+        for b in self.buffers:
+            b.free()
+        self.buffers = []
+
+
+def prepare_gemm(rt, m, n, k, keep=False):
     a = jade_hip.fill_values(m * k, 0x12345678, 1.0)
     b = jade_hip.fill_values(k * n, 0x9ABCDEF1, 1.0)
     kernel = rt.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
@@ -80,60 +164,110 @@ def bench_gemm(rt, m, n, k, steps, warmup, keep=False):
     rt.upload(ag, a)
     rt.upload(bg, b)
     upload_ms = (time.perf_counter() - started) * 1000.0
-    ms, wall = timed(rt, [(kernel, [ag, bg, cg])], steps, warmup)
+    info = {"m": m, "n": n, "k": k, "flop": 2.0 * m * n * k, "kernel": kernel.launch["kernel"],
+            "launch": kernel.launch, "upload_ms": upload_ms}
+    p = Prepared(rt, [(kernel, [ag, bg, cg])], [ag, bg, cg], info)
+    p.keep = (a, b) if keep else None
+    p.output = cg
+    return p
+
+
+def finish_gemm(rt, p, timing):
+    info = dict(p.info)
+    info.update(timing)
     started = time.perf_counter()
-    c = rt.download(cg)
-    download_ms = (time.perf_counter() - started) * 1000.0
-    flops = 2.0 * m * n * k
-    out = {"m": m, "n": n, "k": k, "ms_per_step": ms, "wall_ms_per_step": wall,
-           "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"], "launch": kernel.launch,
-           "upload_ms": upload_ms, "download_ms": download_ms,
-           "pcie_inclusive_tflops": flops / ((ms + upload_ms + download_ms) * 1e-3) / 1e12}
-    if keep:
-        out["_data"] = (a, b, c)
-    for x in (ag, bg, cg):
-        x.free()
-    return out
+    c = rt.download(p.output)
+    info["download_ms"] = (time.perf_counter() - started) * 1000.0
+    ms = timing["ms_per_step"]
+    info["tflops"] = info["flop"] / (ms * 1e-3) / 1e12
+    info["pcie_inclusive_tflops"] = info["flop"] / ((ms + info["upload_ms"] + info["download_ms"]) * 1e-3) / 1e12
+    if p.keep is not None:
+        info["_data"] = p.keep + (c,)
+    p.close()
+    return info
 
 
-def bench_attention(rt, heads, seq, dim, causal, steps, warmup, keep=False):
+def prepare_attention(rt, heads, seq, dim, causal, keep=False):
     n = heads * seq * dim
     q = jade_hip.fill_normal(n, 0x1111)
     k = jade_hip.fill_normal(n, 0x2222)
     v = jade_hip.fill_normal(n, 0x3333)
     kernel = rt.compile({"op": "attention_online", "heads": heads, "seq": seq, "dim": dim, "causal": causal})
     bufs = [rt.resident(x) for x in (q, k, v)] + [rt.alloc(n)]
-    ms, wall = timed(rt, [(kernel, bufs)], steps, warmup)
     keys = seq * (seq + 1) // 2 if causal else seq * seq
-    flops = 4.0 * heads * dim * keys
-    out = {"heads": heads, "seq": seq, "dim": dim, "causal": causal, "flop": flops, "ms_per_step": ms,
-           "wall_ms_per_step": wall, "tflops": flops / (ms * 1e-3) / 1e12, "kernel": kernel.launch["kernel"],
-           "launch": kernel.launch}
-    if keep:
-        out["_data"] = (q, k, v, rt.download(bufs[3]))
-    for x in bufs:
-        x.free()
-    return out
+    info = {"heads": heads, "seq": seq, "dim": dim, "causal": causal, "flop": 4.0 * heads * dim * keys,
+            "kernel": kernel.launch["kernel"], "launch": kernel.launch}
+    p = Prepared(rt, [(kernel, bufs)], bufs, info)
+    p.keep = (q, k, v) if keep else None
+    p.output = bufs[3]
+    return p
+
+
+def finish_attention(rt, p, timing):
+    info = dict(p.info)
+    info.update(timing)
+    info["tflops"] = info["flop"] / (timing["ms_per_step"] * 1e-3) / 1e12
+    if p.keep is not None:
+        info["_data"] = p.keep + (rt.download(p.output),)
+    p.close()
+    return info
+
+
+def bench_gemm(rt, m, n, k, steps, warmup, keep=False):
+    p = prepare_gemm(rt, m, n, k, keep)
+    return finish_gemm(rt, p, measure({"gemm": p.workload}, steps, warmup)["gemm"])
+
+
+def bench_attention(rt, heads, seq, dim, causal, steps, warmup, keep=False):
+    p = prepare_attention(rt, heads, seq, dim, causal, keep)
+    return finish_attention(rt, p, measure({"attention": p.workload}, steps, warmup)["attention"])
+
+
+def rotated(rt, spec, inputs, n_out, nbytes, min_total=3 * MALL_BYTES):
+    """A bandwidth op launched over enough copies of its inputs and output that
+    one step's footprint is at least `min_total` bytes (three times the MALL),
+    so every launch streams from HBM rather than from the cache. One step is
+    one launch per copy."""
+    kernel = rt.compile(spec)
+    sets = max(1, -(-int(min_total) // int(nbytes)))
+    jobs, bufs = [], []
+    for _ in range(sets):
+        b = [rt.resident(t) for t in inputs] + [rt.alloc(n_out)]
+        bufs += b
+        jobs.append((kernel, b))
+    info = {"bytes": nbytes, "kernel": kernel.launch["kernel"], "copies": sets,
+            "footprint_bytes": sets * nbytes}
+    return Prepared(rt, jobs, bufs, info, launches=sets)
+
+
+def finish_rotated(p, timing):
+    info = dict(p.info)
+    ms = timing["ms_per_launch"]
+    info.update({"ms": ms, "gbps": info["bytes"] / (ms * 1e-3) / 1e9,
+                 "frac_hbm": info["bytes"] / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS,
+                 "samples": timing["samples"], "preheat_ms": timing["preheat_ms"]})
+    p.close()
+    return info
 
 
 def bench_softmax(rt, rows, cols, steps, warmup):
     x = jade_hip.fill_normal(rows * cols, 0x6666, 0.0, 2.0)
-    kernel = rt.compile({"op": "softmax", "rows": rows, "cols": cols})
-    xg, og = rt.resident(x), rt.alloc(rows * cols)
-    ms, wall = timed(rt, [(kernel, [xg, og])], steps, warmup)
     nbytes = 2.0 * rows * cols * 4
-    for b in (xg, og):
-        b.free()
-    return {"rows": rows, "cols": cols, "bytes": nbytes, "ms_per_step": ms, "wall_ms_per_step": wall,
-            "gbps": nbytes / (ms * 1e-3) / 1e9, "kernel": kernel.launch["kernel"]}
+    p = rotated(rt, {"op": "softmax", "rows": rows, "cols": cols}, (x,), rows * cols, nbytes)
+    out = finish_rotated(p, measure({"softmax": p.workload}, steps, warmup)["softmax"])
+    out.update({"rows": rows, "cols": cols})
+    return out
+
+
+MLP_SEEDS = {"x": 0x1234, "gamma": 0x7777, "wg": 0x3333, "wu": 0x4444, "wd": 0x5555}
 
 
 def bench_mlp(rt, batch, width, hidden, steps, warmup):
-    x = jade_hip.fill_normal(batch * width, 0x1234)
-    gamma = jade_hip.fill_values(width, 0x7777, 0.5) + np.float32(1.0)
-    wg = jade_hip.fill_normal(width * hidden, 0x3333, 0.0, 0.02)
-    wu = jade_hip.fill_normal(width * hidden, 0x4444, 0.0, 0.02)
-    wd = jade_hip.fill_normal(hidden * width, 0x5555, 0.0, 0.02)
+    x = jade_hip.fill_normal(batch * width, MLP_SEEDS["x"])
+    gamma = jade_hip.fill_values(width, MLP_SEEDS["gamma"], 0.5) + np.float32(1.0)
+    wg = jade_hip.fill_normal(width * hidden, MLP_SEEDS["wg"], 0.0, 0.02)
+    wu = jade_hip.fill_normal(width * hidden, MLP_SEEDS["wu"], 0.0, 0.02)
+    wd = jade_hip.fill_normal(hidden * width, MLP_SEEDS["wd"], 0.0, 0.02)
     specs = [
         ("rms_norm", {"op": "rms_norm", "rows": batch, "cols": width, "epsilon": 1e-6}),
         ("gemm_gate", {"op": "gemm", "m": batch, "n": hidden, "k": width, "tiled": True}),
@@ -149,33 +283,31 @@ def bench_mlp(rt, batch, width, hidden, steps, warmup):
     jobs = [(kernels[0], [xg, ng, normalized]), (kernels[1], [normalized, wgg, gate]),
             (kernels[2], [normalized, wug, up]), (kernels[3], [gate, up, act]), (kernels[4], [act, wdg, proj]),
             (kernels[5], [proj, xg, out])]
-    block_ms, block_wall = timed(rt, jobs, steps, warmup)
-    per = {}
-    bw_bytes = {"rms_norm": (2.0 * batch * width + width) * 4, "swiglu": 3.0 * batch * hidden * 4,
-                "add": 3.0 * batch * width * 4}
+    block = measure({"block": Workload(rt, jobs)}, steps, warmup)["block"]
     gemm_flops = {"gemm_gate": 2.0 * batch * hidden * width, "gemm_up": 2.0 * batch * hidden * width,
                   "gemm_down": 2.0 * batch * width * hidden}
+    per = {}
     for (name, _), job in zip(specs, jobs):
-        ms, _ = timed(rt, [job], steps, warmup)
-        entry = {"ms": ms}
-        if name in bw_bytes:
-            entry["gbps"] = bw_bytes[name] / (ms * 1e-3) / 1e9
-            entry["frac_hbm"] = entry["gbps"] / PEAK_HBM_GBPS
-        else:
-            entry["tflops"] = gemm_flops[name] / (ms * 1e-3) / 1e12
-            entry["frac_mfma"] = entry["tflops"] / PEAK_FP32_MFMA_TFLOPS
-        per[name] = entry
+        if name in gemm_flops:
+            t = measure({name: Workload(rt, [job])}, steps, warmup)[name]
+            ms = t["ms_per_step"]
+            per[name] = {"ms": ms, "tflops": gemm_flops[name] / (ms * 1e-3) / 1e12,
+                         "frac_mfma": gemm_flops[name] / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS}
     total_flops = sum(gemm_flops.values())
     for buf in (xg, ng, wgg, wug, wdg, normalized, gate, up, act, proj, out):
         buf.free()
-    return {"batch": batch, "width": width, "hidden": hidden, "ms_per_block": block_ms,
-            "wall_ms_per_block": block_wall, "gemm_tflops_block": total_flops / (block_ms * 1e-3) / 1e12,
-            "per_op": per}
+    # The bandwidth ops alone at the MLP shapes, streaming from HBM.
+    per.update(bench_rows(rt, batch, width, hidden, steps, warmup))
+    return {"batch": batch, "width": width, "hidden": hidden, "ms_per_block": block["ms_per_step"],
+            "block_timing": block, "gemm_tflops_block": total_flops / (block["ms_per_step"] * 1e-3) / 1e12,
+            "seeds": {k: hex(v) for k, v in MLP_SEEDS.items()}, "per_op": per}
 
 
 def bench_rows(rt, batch, width, hidden, steps, warmup):
-    """The MLP's bandwidth-bound ops launched one at a time at the MLP shapes,
-    with the MLP's inputs (the counter runs read HBM bytes per kernel)."""
+    """RMSNorm, SwiGLU and Add launched alone at the MLP shapes, each rotated
+    over copies of its buffers totalling at least three times the MALL, so the
+    bytes come from HBM (a launch re-reading one 16-50 MB input would be
+    served by the 256 MB cache)."""
     x = jade_hip.fill_normal(batch * width, 0x1234)
     gamma = jade_hip.fill_values(width, 0x7777, 0.5) + np.float32(1.0)
     gate = jade_hip.fill_normal(batch * hidden, 0x2468)
@@ -189,14 +321,8 @@ def bench_rows(rt, batch, width, hidden, steps, warmup):
     ]
     out = {}
     for name, spec, inputs, n_out, nbytes in cases:
-        kernel = rt.compile(spec)
-        bufs = [rt.resident(t) for t in inputs] + [rt.alloc(n_out)]
-        ms, _ = timed(rt, [(kernel, bufs)], steps, warmup)
-        for b in bufs:
-            b.free()
-        gbps = nbytes / (ms * 1e-3) / 1e9
-        out[name] = {"ms": ms, "bytes": nbytes, "gbps": gbps, "frac_hbm": gbps / PEAK_HBM_GBPS,
-                     "kernel": kernel.launch["kernel"]}
+        p = rotated(rt, spec, inputs, n_out, nbytes)
+        out[name] = finish_rotated(p, measure({name: p.workload}, steps, warmup)[name])
     return out
 
 
@@ -204,17 +330,15 @@ COPY_ELEMENTS = 1 << 26  # 256 MiB read + 256 MiB written per launch
 
 
 def bench_copy(rt, steps, warmup):
-    """A plain copy of known size: the calibration point for the HBM counters."""
+    """A plain copy of known size: the calibration point for the HBM counters
+    and the practical streaming ceiling, rotated over two source/destination
+    pairs (1 GiB) so it streams from HBM."""
     n = COPY_ELEMENTS
     spec = {"op": "elementwise", "len": n, "inputs": 1, "expression": {"kind": "input", "binding": 0}}
-    kernel = rt.compile(spec)
-    src, dst = rt.resident(jade_hip.fill_values(n, 0x4242, 1.0)), rt.alloc(n)
-    ms, wall = timed(rt, [(kernel, [src, dst])], steps, warmup)
-    for b in (src, dst):
-        b.free()
-    nbytes = 2.0 * n * 4
-    return {"elements": n, "bytes": nbytes, "ms_per_step": ms, "gbps": nbytes / (ms * 1e-3) / 1e9,
-            "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, "kernel": kernel.launch["kernel"]}
+    p = rotated(rt, spec, (jade_hip.fill_values(n, 0x4242, 1.0),), n, 2.0 * n * 4)
+    out = finish_rotated(p, measure({"copy": p.workload}, steps, warmup)["copy"])
+    out["elements"] = n
+    return out
 
 
 def _read_csv(path):
@@ -340,12 +464,35 @@ def summarize_mfma(directory):
     return "\n".join(lines)
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the OpenMP oracle: every CPU this process may run on, capped
+    by OMP_NUM_THREADS where the host sets it (the GPU pool sets it to the
+    16-thread CPU share of one GPU)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(usable, int(cap))) if cap.isdigit() and int(cap) > 0 else max(1, usable)
+
+
 def cpu_baseline(gemm, attention):
     """The reference's CPU path (FP64 oracle loops) on this host, bounded sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_binding as orc
 
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = cpu_threads()
     a, b, c_gpu = gemm["_data"]
     m, n, k = gemm["m"], gemm["n"], gemm["k"]
     rows = max(1, min(m, int(os.environ.get("JADE_CPU_ROWS", str(m)))))
@@ -359,9 +506,11 @@ def cpu_baseline(gemm, attention):
     single_s = time.perf_counter() - started
     gemm_flop = 2.0 * rows * n * k
     out = {"value": gemm_flop / omp_s / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+           "cpu_model": cpu_model(), "host_logical_cpus": os.cpu_count(),
            "sample": f"FP64 gemm_reference (metal_lab.rs:18-31) rows 0..{rows} of the {m}x{n}x{k} GEMM "
                      f"({gemm_flop:.3e} FLOP, {omp_s:.2f} s on {cores} OpenMP threads)",
            "single_thread_tflops": 2.0 * single_rows * n * k / single_s / 1e12,
+           "single_thread_sample": f"rows 0..{single_rows}, {single_s:.2f} s",
            "gpu_check_rows": rows, "gpu_check_status": int(check.status),
            "gpu_max_abs_error": check.max_abs_error, "gpu_max_rel_error": check.max_relative_error}
     if attention is not None and "_data" in attention:
@@ -383,12 +532,13 @@ def cpu_baseline(gemm, attention):
 
 
 def main():
+    global PREHEAT_MS
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # The MI355X clock ramps up over the first ~30 ms of sustained matrix work;
-    # 50 untimed 4096^3 steps (~55 ms) reach the steady state before timing.
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--preheat-ms", type=float, default=PREHEAT_MS,
+                    help="untimed device time of each workload before its samples (0 for counter runs)")
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -417,39 +567,50 @@ def main():
         print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
-    if args.steps <= 0 or args.warmup < 0:
-        sys.exit("steps must be positive and warmup non-negative")
+    if args.steps <= 0 or args.warmup < 0 or args.preheat_ms < 0:
+        sys.exit("steps must be positive, warmup and preheat non-negative")
+    PREHEAT_MS = args.preheat_ms
 
     rt = jade_hip.HipRuntime(0)
     log(f"device: {rt.device_info}")
     K, W, wl = args.steps, args.warmup, args.workload
     extra = {}
     gemm = attention = None
-    if wl in ("all", "gemm"):
-        log("gemm 4096^3 ...")
-        gemm = bench_gemm(rt, 4096, 4096, 4096, K, W, keep=not args.no_cpu_baseline)
-        log(f"  {gemm['tflops']:.2f} TFLOP/s")
+    keep = not args.no_cpu_baseline
+    if wl in ("all", "gemm", "attention"):
+        # The two headline kernels, sampled interleaved (round r rotates the order).
+        heads = {}
+        if wl in ("all", "gemm"):
+            heads["gemm"] = prepare_gemm(rt, 4096, 4096, 4096, keep)
+        if wl in ("all", "attention"):
+            heads["attention"] = prepare_attention(rt, 128, 4096, 128, True, keep)
+        log(f"headline {', '.join(heads)} ...")
+        timing = measure({name: p.workload for name, p in heads.items()}, K, W)
+        if "gemm" in heads:
+            gemm = finish_gemm(rt, heads["gemm"], timing["gemm"])
+            log(f"  gemm 4096^3 {gemm['tflops']:.2f} TFLOP/s")
+        if "attention" in heads:
+            attention = finish_attention(rt, heads["attention"], timing["attention"])
+            log(f"  attention B4 H32 S4096 D128 causal {attention['tflops']:.2f} TFLOP/s")
     if wl in ("all", "attention"):
-        log("attention B4 H32 S4096 D128 causal ...")
-        # ~4.7 ms per launch: a fifth of the GEMM step counts covers the same time.
-        attention = bench_attention(rt, 128, 4096, 128, True, max(1, K // 5), max(1, W // 5),
-                                    keep=not args.no_cpu_baseline)
-        log(f"  {attention['tflops']:.2f} TFLOP/s")
         c3 = {}
         for causal in (False, True):
             r = bench_attention(rt, 8, 1024, 64, causal, K, W)
-            c3["causal" if causal else "noncausal"] = {"ms": r["ms_per_step"], "tflops": r["tflops"]}
+            c3["causal" if causal else "noncausal"] = {
+                "ms": r["ms_per_step"], "tflops": r["tflops"], "frac_mfma": r["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+                "min_ms": r["min_ms_per_step"], "max_ms": r["max_ms_per_step"], "kernel": r["kernel"]}
         extra["attention_c3_b1h8s1024d64"] = c3
+        log(f"  C3 {c3['noncausal']['tflops']:.1f} / {c3['causal']['tflops']:.1f} TFLOP/s")
     if wl in ("all", "softmax"):
         log("softmax 32768x4096 ...")
         sm = bench_softmax(rt, 32768, 4096, K, W)
-        sm["frac_hbm"] = sm["gbps"] / PEAK_HBM_GBPS
         extra["softmax_32768x4096"] = sm
         log(f"  {sm['gbps']:.0f} GB/s")
     if wl in ("all", "mlp"):
         log("six-op MLP 4096x1024x2816 ...")
         extra["mlp_4096x1024x2816"] = bench_mlp(rt, 4096, 1024, 2816, K, W)
-    if wl == "rows":  # counter runs only; the default line times these ops inside the MLP block
+        log(f"  {extra['mlp_4096x1024x2816']['ms_per_block']:.3f} ms per block")
+    if wl == "rows":  # counter runs only; the default line measures these ops inside bench_mlp
         extra["rows_mlp_shapes"] = bench_rows(rt, 4096, 1024, 2816, K, W)
     if wl in ("all", "copy"):
         extra["copy_calibration"] = bench_copy(rt, K, W)
@@ -459,12 +620,12 @@ def main():
         sweep = {}
         for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
                         (4096, 11008, 4096)):
-            # Short launches get enough warm-up steps to cover the clock ramp
-            # (~40 ms at an assumed 100 TFLOP/s).
-            warm = max(W, int(40e-3 / (2.0 * m * n * k / 100e12)))
-            r = bench_gemm(rt, m, n, k, K if m * n * k < 1 << 36 else max(2, K // 2), warm)
+            r = bench_gemm(rt, m, n, k, K, W)
             sweep[f"{m}x{n}x{k}"] = {"ms": r["ms_per_step"], "tflops": r["tflops"],
-                                     "frac_mfma": r["tflops"] / PEAK_FP32_MFMA_TFLOPS}
+                                     "frac_mfma": r["tflops"] / PEAK_FP32_MFMA_TFLOPS,
+                                     "min_ms": r["min_ms_per_step"], "max_ms": r["max_ms_per_step"],
+                                     "kernel": r["kernel"]}
+            log(f"  sweep {m}x{n}x{k} {r['tflops']:.1f} TFLOP/s")
         extra["gemm_sweep"] = sweep
 
     head = gemm or attention
@@ -472,14 +633,14 @@ def main():
         print(json.dumps({"metric": METRIC, "workload": wl, "extra": extra}))
         return
     if gemm is not None:
-        flop_per_launch = 2.0 * gemm["m"] * gemm["n"] * gemm["k"]
         config = {"workload": "FP32 GEMM C=A.B 4096x4096x4096, row-major (BASELINE configs[1] headline)",
                   "m": 4096, "n": 4096, "k": 4096,
                   "inputs": "validation::inputs xorshift32 seeds 0x12345678/0x9abcdef1, U[-1,1)"}
+        symbol = "gemm_f32_mfma"
     else:
-        flop_per_launch = attention["flop"]
         config = {"workload": "FP32 causal attention B4 H32 S4096 D128 (BASELINE configs[4])"}
-    achieved = flop_per_launch / (head["ms_per_step"] * 1e-3) / 1e12
+        symbol = "attention_online_mfma"
+    achieved = head["flop"] / (head["ms_per_step"] * 1e-3) / 1e12
     line = {
         "metric": METRIC,
         "value": head["tflops"],
@@ -494,12 +655,17 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": config,
+        "timing": {"method": f"median of {head['samples']} interleaved samples over the {K} timed steps, after "
+                             f"{W} warm-up steps and a {PREHEAT_MS:.0f} ms time-based pre-heat per workload",
+                   "median_ms_per_step": head["ms_per_step"], "mean_ms_per_step": head["mean_ms_per_step"],
+                   "min_ms_per_step": head["min_ms_per_step"], "max_ms_per_step": head["max_ms_per_step"],
+                   "sample_steps": head["sample_steps"]},
+        "preheat_ms": head["preheat_ms"],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-                     "traffic": traffic_from_profiles(
-                         "gemm_f32_mfma" if gemm is not None else "attention_online_mfma", head["launch"])},
+                     "traffic": traffic_from_profiles(symbol, head["launch"])},
     }
-    if attention is not None:
+    if attention is not None and gemm is not None:
         att = {k: v for k, v in attention.items() if not k.startswith("_")}
         att["roofline"] = {"bound": "mfma", "achieved": attention["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                            "unit": "TFLOP/s", "frac": attention["tflops"] / PEAK_FP32_MFMA_TFLOPS,

@@ -37,20 +37,23 @@ typedef struct jr_job {
 /* native/jade_runtime_corex.h:18 (corex.rs:263-266 checks it). Returns 2. */
 uint32_t jr_version(void);
 
-/* native/jade_runtime_corex.h:19 / jade_runtime_corex.cpp:47-71: selects the
- * device, creates one non-blocking stream (default priority) and two events. */
+/* native/jade_runtime_corex.h:19: opens a context on `device`: one ordered
+ * non-blocking queue (default priority), an event pair for timing and an
+ * empty region table. */
 int jr_create(int device, void **out, char *err, size_t cap);
 
 /* native/jade_runtime_corex.h:20: synchronises, releases kernels, allocations,
  * events and the stream. Null-safe. */
 void jr_destroy(void *ctx);
 
-/* native/jade_runtime_corex.h:21: "device=%d name=... memory_bytes=...
- * runtime_api=%d driver_api=%d" followed by " arch=... compute_units=...". */
+/* native/jade_runtime_corex.h:21: one line naming the device, e.g.
+ * "hip:0 AMD Instinct MI355X isa=gfx950:sramecc+:xnack- cus=256
+ * hbm_bytes=... hip_runtime=... hip_driver=...". The text is informational
+ * (the reference's caller stores it verbatim: corex.rs:305). */
 int jr_info(void *ctx, char *out, size_t out_cap, char *err, size_t cap);
 
-/* native/jade_runtime_corex.h:22 / jade_runtime_corex.cpp:97-116: nonempty,
- * zero-initialised device allocation registered with this context. */
+/* native/jade_runtime_corex.h:22: a nonempty device region that reads as
+ * zeros before its first upload, recorded in this context's region table. */
 int jr_alloc(void *ctx, size_t bytes, void **out, char *err, size_t cap);
 
 /* native/jade_runtime_corex.h:23: synchronises, then frees. Pointers this

@@ -1353,45 +1353,120 @@ Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int 
     return all_interior ? kDmaOnly : kMixed;
 }
 
+// Whether gemm_f32_mfma has an instantiation for a tile of tm x tn MFMA
+// blocks per wave, kg K groups and a load path. The host instantiates
+// 64x64, 128x64 and 128x128 tiles with one group and 64x64 tiles with two or
+// four; the buffer-load unaligned loop exists for tiles of at most two blocks
+// per wave, and the clamped unaligned loop for at most two K groups.
+bool tile_instantiated(int tm, int tn, int kg, Path path, bool vec) {
+    const bool shape = kg == 1 ? ((tm == 1 && tn == 1) || (tm == 2 && tn == 1) || (tm == 2 && tn == 2))
+                               : (tm == 1 && tn == 1 && (kg == 2 || kg == 4));
+    if (!shape) return false;
+    switch (path) {
+        case kDmaOnly:
+        case kRegOnly: return vec;
+        case kUnalignedBuf: return !vec && tm * tn <= 2;
+        case kMixed: return vec || kg <= 2;
+    }
+    return false;
+}
+
+// The launch gemm_f32 makes for one product shape: its plan and, for the
+// four-wave tile kernel, the K-group count and load path. gemm_f32 and
+// gemm_f32_shape both take their decision from here, so the kernel a
+// description names is the one that runs. `launchable` is false only where
+// no instantiation fits; gemm_f32 then returns hipErrorInvalidValue instead
+// of launching nothing.
+struct Route {
+    Plan plan;
+    bool vec;              // rows of A and B are 16-byte runs (k % 4 == 0, n % 4 == 0)
+    int kg;                // tile kernel: K groups
+    Path path;             // tile kernel: load path
+    bool launchable;
+    bool needs_workspace;  // split-K partials go through the caller's workspace
+};
+
+Route route_for(uint32_t m, uint32_t n, uint32_t k) {
+    Route r{plan_for(m, n, k), k % 4 == 0 && n % 4 == 0, 1, kMixed, m > 0 && n > 0 && k > 0, false};
+    const Plan &p = r.plan;
+    r.needs_workspace = p.slices > 1;
+    if (p.big) {
+        r.launchable = r.launchable && r.vec;  // big_fits implies n % 256 == 0 and k % 32 == 0
+        return r;
+    }
+    if (p.direct) {
+        r.launchable = r.launchable && k % 4 == 0 && (p.slices == 1 || p.direct == 4);
+        return r;
+    }
+    // A four-group plan whose loads would take the clamped global loads
+    // (operands of 2 GiB or more with unaligned rows) runs two groups.
+    r.kg = p.kgroups == 4 && (r.vec || unaligned_buffers_fit(m, n, k)) ? 4 : p.kgroups >= 2 ? 2 : 1;
+    r.path = tile_path(p, r.vec, m, n, k, p.tm, p.tn, r.kg);
+    r.launchable = r.launchable && tile_instantiated(p.tm, p.tn, r.kg, r.path, r.vec);
+    return r;
+}
+
+template <int TM, int TN, int KG, Path PATH, bool VEC>
+hipError_t launch_instance(hipStream_t stream, const Plan &p, dim3 grid, dim3 block, const float *a, const float *b,
+                           float *out, uint32_t m, uint32_t n, uint32_t k, const PairArgs &pair) {
+    hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, VEC, PATH, KG>), grid, block, 0, stream, a, b, out, int(m), int(n),
+                       int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+    return hipGetLastError();
+}
+
+// Launches the four-wave tile kernel for the route's (path, vec) on a
+// TM x TN x KG instantiation; hipErrorInvalidValue when that combination has
+// no instantiation (tile_instantiated).
 template <int TM, int TN, int KG = 1>
-void launch_tile(hipStream_t stream, const Plan &p, bool vec, const float *a, const float *b, float *out,
-                 uint32_t m, uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
+hipError_t launch_tile(hipStream_t stream, const Route &r, const float *a, const float *b, float *out, uint32_t m,
+                       uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
+    const Plan &p = r.plan;
+    if (!tile_instantiated(TM, TN, KG, r.path, r.vec)) return hipErrorInvalidValue;
     const unsigned groups = unsigned(p.tiles_m) * unsigned(p.tiles_n) * (pair.tiles > 0 ? 2u : 1u);
     const dim3 grid(groups, unsigned(p.slices)), block(kThreads * KG);
-    switch (tile_path(p, vec, m, n, k, TM, TN, KG)) {
-        case kDmaOnly:
-            hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kDmaOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
-                               int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-            break;
-        case kRegOnly:
-            hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kRegOnly, KG>), grid, block, 0, stream, a, b, out, int(m),
-                               int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-            break;
+    switch (r.path) {
+        case kDmaOnly: return launch_instance<TM, TN, KG, kDmaOnly, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
+        case kRegOnly: return launch_instance<TM, TN, KG, kRegOnly, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
         case kUnalignedBuf:
             if constexpr (TM * TN <= 2)
-                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kUnalignedBuf, KG>), grid, block, 0, stream, a, b, out,
-                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+                return launch_instance<TM, TN, KG, kUnalignedBuf, false>(stream, p, grid, block, a, b, out, m, n, k,
+                                                                          pair);
             break;
-        default:
-            if (vec)
-                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, true, kMixed, KG>), grid, block, 0, stream, a, b, out,
-                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
-            else if constexpr (KG <= 2)  // the clamped loop runs at most two groups
-                hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, false, kMixed, KG>), grid, block, 0, stream, a, b, out,
-                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+        case kMixed:
+            if (r.vec) return launch_instance<TM, TN, KG, kMixed, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
+            if constexpr (KG <= 2)
+                return launch_instance<TM, TN, KG, kMixed, false>(stream, p, grid, block, a, b, out, m, n, k, pair);
             break;
     }
+    return hipErrorInvalidValue;
 }
+
+// The tile kernel instantiation the route names (one group: 64x64, 128x64,
+// 128x128; two or four groups: 64x64).
+hipError_t launch_route_tiles(hipStream_t stream, const Route &r, const float *a, const float *b, float *out,
+                              uint32_t m, uint32_t n, uint32_t k, PairArgs pair = PairArgs{}) {
+    const Plan &p = r.plan;
+    if (r.kg == 4) return launch_tile<1, 1, 4>(stream, r, a, b, out, m, n, k, pair);
+    if (r.kg == 2) return launch_tile<1, 1, 2>(stream, r, a, b, out, m, n, k, pair);
+    if (p.tm == 2 && p.tn == 2) return launch_tile<2, 2>(stream, r, a, b, out, m, n, k, pair);
+    if (p.tm == 2 && p.tn == 1) return launch_tile<2, 1>(stream, r, a, b, out, m, n, k, pair);
+    if (p.tm == 1 && p.tn == 1) return launch_tile<1, 1>(stream, r, a, b, out, m, n, k, pair);
+    return hipErrorInvalidValue;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
 size_t gemm_f32_workspace_bytes(uint32_t m, uint32_t n, uint32_t k) {
-    const Plan p = plan_for(m, n, k);
-    return p.slices > 1 ? size_t(p.slices) * m * n * sizeof(float) : 0;
+    const Route r = route_for(m, n, k);
+    return r.needs_workspace ? size_t(r.plan.slices) * m * n * sizeof(float) : 0;
 }
 
 LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
-    const Plan p = plan_for(m, n, k);
+    const Route r = route_for(m, n, k);
+    const Plan &p = r.plan;
+    if (!r.launchable) return {nullptr, {0, 0, 0}, {0, 0, 0}, 0};
     if (p.big) {  // the first launch; a partial last round follows as smaller tiles
         const char *name = "gemm_f32_mfma_256x256x32";
         if (p.big_full < p.tiles_m * p.tiles_n)
@@ -1408,10 +1483,10 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     }
     // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
     // run K groups.
-    if (p.kgroups == 4)
+    if (r.kg == 4)
         return {"gemm_f32_mfma_64x64x32_k4", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {4 * kThreads, 1, 1},
                 4 * Tile<1, 1>::kLdsBytes};
-    if (p.kgroups == 2)
+    if (r.kg == 2)
         return {p.slices > 1 ? "gemm_f32_mfma_64x64x32_splitk_k2" : "gemm_f32_mfma_64x64x32_k2",
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {2 * kThreads, 1, 1},
@@ -1429,38 +1504,32 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
 }
 
 bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
-    const Plan p = plan_for(m, n, k);
-    return !p.big && !p.direct && p.kgroups < 2 && p.slices == 1 && m > 0 && n > 0 && k > 0;
+    const Route r = route_for(m, n, k);
+    return r.launchable && !r.plan.big && !r.plan.direct && r.kg == 1 && r.plan.slices == 1;
 }
 
 hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
                          const float *b1, float *c1, uint32_t m, uint32_t n, uint32_t k) {
-    const Plan p = plan_for(m, n, k);
-    if (p.big || p.direct || p.kgroups >= 2 || p.slices != 1) return hipErrorInvalidValue;
-    const uintptr_t bits = reinterpret_cast<uintptr_t>(a0) | reinterpret_cast<uintptr_t>(b0) |
-                           reinterpret_cast<uintptr_t>(a1) | reinterpret_cast<uintptr_t>(b1);
-    const bool vec = (bits & 15u) == 0 && (k % 4 == 0) && (n % 4 == 0);
-    const PairArgs pair{a1, b1, c1, p.tiles_m * p.tiles_n};
-    if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a0, b0, c0, m, n, k, pair);
-    else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
-    else launch_tile<1, 1>(stream, p, vec, a0, b0, c0, m, n, k, pair);
-    return hipGetLastError();
+    if (!gemm_f32_pairable(m, n, k)) return hipErrorInvalidValue;
+    if (!aligned16(a0) || !aligned16(b0) || !aligned16(a1) || !aligned16(b1)) return hipErrorInvalidValue;
+    const Route r = route_for(m, n, k);
+    const PairArgs pair{a1, b1, c1, r.plan.tiles_m * r.plan.tiles_n};
+    return launch_route_tiles(stream, r, a0, b0, c0, m, n, k, pair);
 }
 
 bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
     // The plan the pair would take must be the 128x64 tile, so the fused
     // outputs are the pair's bits.
-    const Plan p = plan_for(m, n, k);
-    return !p.big && !p.direct && p.kgroups < 2 && p.slices == 1 && p.tm == 2 && p.tn == 1 &&
-           m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 && k > 0 &&
-           dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
+    const Route r = route_for(m, n, k);
+    const Plan &p = r.plan;
+    return gemm_f32_pairable(m, n, k) && p.tm == 2 && p.tn == 1 && m % dual::T::kBM == 0 && n % dual::T::kBN == 0 &&
+           k % kBK == 0 && dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
 }
 
 hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,
                                 float *u, float *act, uint32_t m, uint32_t n, uint32_t k) {
-    const uintptr_t bits = reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(bg) |
-                           reinterpret_cast<uintptr_t>(bu);
-    if (!gemm_f32_dual_swiglu_fits(m, n, k) || (bits & 15u) != 0) return hipErrorInvalidValue;
+    if (!gemm_f32_dual_swiglu_fits(m, n, k) || !aligned16(a) || !aligned16(bg) || !aligned16(bu))
+        return hipErrorInvalidValue;
     const int tiles_m = int(m / dual::T::kBM), tiles_n = int(n / dual::T::kBN);
     hipLaunchKernelGGL(gemm_f32_dual_swiglu, dim3(unsigned(tiles_m * tiles_n)), dim3(dual::kThreads), 0, stream, a, bg,
                        bu, g, u, act, int(n), int(k), tiles_m, tiles_n);
@@ -1479,40 +1548,30 @@ hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const flo
 
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
                     uint32_t k, float *workspace) {
-    const Plan p = plan_for(m, n, k);
-    const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15u) == 0;
-    const bool vec = aligned && (k % 4 == 0) && (n % 4 == 0);
-    if (p.slices > 1 && !workspace) return hipErrorInvalidValue;
+    // Operands are whole device regions (256-byte aligned); the kernels'
+    // 16-byte loads rely on the base alignment.
+    if (!aligned16(a) || !aligned16(b)) return hipErrorInvalidValue;
+    const Route r = route_for(m, n, k);
+    if (!r.launchable || (r.needs_workspace && !workspace)) return hipErrorInvalidValue;
+    const Plan &p = r.plan;
     if (p.big) {
-        if (vec) {
-            hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.big_full)), dim3(big::kThreads), 0, stream, a, b, c,
-                               int(m), int(n), int(k), p.tiles_m, p.tiles_n);
-            const int tail = p.tiles_m * p.tiles_n - p.big_full;
-            if (tail > 0) {
-                const dim3 grid(unsigned(tail * (4 / p.tail_tm) * (4 / p.tail_tn)));
-                if (p.tail_tm == 1)
-                    hipLaunchKernelGGL((gemm_f32_mfma<1, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
-                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
-                else
-                    hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
-                                       int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
-            }
-            return hipGetLastError();
+        hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.big_full)), dim3(big::kThreads), 0, stream, a, b, c,
+                           int(m), int(n), int(k), p.tiles_m, p.tiles_n);
+        const int tail = p.tiles_m * p.tiles_n - p.big_full;
+        if (tail > 0) {
+            const dim3 grid(unsigned(tail * (4 / p.tail_tm) * (4 / p.tail_tn)));
+            if (p.tail_tm == 1)
+                hipLaunchKernelGGL((gemm_f32_mfma<1, 1, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
+                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
+            else
+                hipLaunchKernelGGL((gemm_f32_mfma<2, 2, true, kDmaOnly>), grid, dim3(kThreads), 0, stream, a, b, c,
+                                   int(m), int(n), int(k), p.tiles_m, p.tiles_n, int(k), p.big_full, PairArgs{});
         }
-        // Unaligned pointers: the 128x128 register-staged path (no split: the
-        // grid is large).
-        const Plan q{2, 2, 1, int(k), int(m / 128), int(n / 128), false, 0, 0, 1, 0, 0};
-        launch_tile<2, 2>(stream, q, false, a, b, c, m, n, k);
         return hipGetLastError();
     }
     if (p.direct) {
         const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
-        if ((reinterpret_cast<uintptr_t>(a) & 15u) != 0) {
-            // Unaligned A: the 64x64 register-staged tiles (no split).
-            const Plan q{1, 1, 1, int(((k + kBK - 1) / kBK) * kBK), int((m + 63) / 64), int((n + 63) / 64), false, 0, 0,
-                         1, 0, 0};
-            launch_tile<1, 1>(stream, q, false, a, b, c, m, n, k);
-        } else if (p.slices > 1) {
+        if (p.slices > 1) {
             // K slices of p.kchunk (which divides K) as a batch of products
             // into the workspace, then the ordered reduce.
             const size_t mn = size_t(m) * n;
@@ -1536,15 +1595,7 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         return hipGetLastError();
     }
     float *out = p.slices > 1 ? workspace : c;
-    // A four-group plan whose loads would take the clamped global loads
-    // (pointers not 16-byte aligned, operands of 2 GiB or more) runs two groups.
-    if (p.kgroups == 4 && (vec || unaligned_buffers_fit(m, n, k)))
-        launch_tile<1, 1, 4>(stream, p, vec, a, b, out, m, n, k);
-    else if (p.kgroups >= 2) launch_tile<1, 1, 2>(stream, p, vec, a, b, out, m, n, k);
-    else if (p.tm == 2 && p.tn == 2) launch_tile<2, 2>(stream, p, vec, a, b, out, m, n, k);
-    else if (p.tm == 2) launch_tile<2, 1>(stream, p, vec, a, b, out, m, n, k);
-    else launch_tile<1, 1>(stream, p, vec, a, b, out, m, n, k);
-    hipError_t status = hipGetLastError();
+    const hipError_t status = launch_route_tiles(stream, r, a, b, out, m, n, k);
     if (status != hipSuccess || p.slices == 1) return status;
     const size_t mn = size_t(m) * n;
     const unsigned groups = unsigned((mn + 1023) / 1024);

@@ -1,71 +1,78 @@
-// Per-shape GEMM-plan ABI (native/jade_corex.h:11-29) over this library's FP32
-// MFMA GEMM: one context holds M,N,K, device A/B/C, a non-blocking stream and
-// two events; run() replays the product `iterations` times between events.
-// Mirrors the state machine of native/jade_corex.cpp:113-291 (upload before
-// run, run before download, exact element counts).
-#include <hip/hip_runtime.h>
-
-#include <climits>
-#include <cmath>
-#include <cstdarg>
-#include <cstdio>
-#include <limits>
-#include <new>
+// The per-shape GEMM-plan C ABI (names, signatures and codes of
+// native/jade_corex.h:11-29), written as a client of this library's own jr_*
+// runtime rather than as a second device layer. A plan is:
+//   - one runtime context (jr_create),
+//   - three regions A [m,k], B [k,n], C [m,n] (jr_alloc),
+//   - one compiled `gemm` pipeline (jr_compile of the KernelSpec
+//     {"op":"gemm","m":m,"n":n,"k":k,"tiled":true}, so the IR's shape rules
+//     and its 31-bit element bound per matrix apply unchanged),
+// and run() is one jr_execute_dispatches batch of that single job replayed
+// `iterations` times. The product is this library's FP32 MFMA kernel.
+//
+// Codes: 1 invalid input or order of calls, 2 device, 4 allocation. Code 3
+// (a BLAS failure in the reference) cannot occur: no BLAS is called.
+#include <memory>
+#include <string>
 
 #include "jade_gemm_hip.h"
-#include "kernels.hpp"
+#include "jade_runtime_hip.h"
+#include "session.hpp"
 
 namespace {
 
-struct Plan {
-    int m = 0, n = 0, k = 0, device = 0;
-    size_t a_len = 0, b_len = 0, c_len = 0;
-    float *a = nullptr, *b = nullptr, *c = nullptr;
-    float *workspace = nullptr;  // split-K partials for small output grids
-    hipStream_t stream = nullptr;
-    hipEvent_t start = nullptr, stop = nullptr;
-    bool uploaded = false, computed = false;
+using jade::dev::Kind;
+using jade::dev::refuse;
+using jade::dev::refuse_invalid;
+using jade::dev::text_of;
+
+int plan_code(Kind kind) {
+    switch (kind) {
+        case Kind::Invalid: return 1;
+        case Kind::Device: return 2;
+        case Kind::Memory: return 4;
+    }
+    return 2;
+}
+
+template <class Body>
+int entry(char *err, size_t cap, Body &&body) {
+    return jade::dev::abi_entry(err, cap, plan_code, body);
+}
+
+// Rethrows a failed jr_* call (codes 1/2/3) as this ABI's refusal, keeping
+// the runtime's message.
+void forward(int jr_status, const char *why) {
+    if (jr_status == 0) return;
+    const Kind kind = jr_status == 1 ? Kind::Invalid : jr_status == 3 ? Kind::Memory : Kind::Device;
+    refuse(kind, why);
+}
+
+struct GemmPlan {
+    uint32_t m = 0, n = 0, k = 0;
+    void *runtime = nullptr;
+    void *kernel = nullptr;
+    void *a = nullptr, *b = nullptr, *c = nullptr;
+    // What the device regions hold: nothing usable, the operands of the last
+    // successful upload, or those operands and their product.
+    enum class Holds { Nothing, Operands, Product } holds = Holds::Nothing;
+
+    size_t a_len() const { return size_t(m) * k; }
+    size_t b_len() const { return size_t(k) * n; }
+    size_t c_len() const { return size_t(m) * n; }
+
+    ~GemmPlan() {
+        if (!runtime) return;
+        jr_kernel_release(runtime, kernel);
+        jr_destroy(runtime);  // frees A, B and C with the context
+    }
 };
 
-void clear_error(char *err, size_t cap) {
-    if (err && cap) err[0] = '\0';
-}
-int fail(int code, char *err, size_t cap, const char *format, ...) {
-    if (err && cap) {
-        va_list args;
-        va_start(args, format);
-        std::vsnprintf(err, cap, format, args);
-        va_end(args);
-        err[cap - 1] = '\0';
-    }
-    return code;
-}
-int runtime_error(hipError_t status, char *err, size_t cap, const char *op) {
-    return fail(2, err, cap, "%s: %s (runtime code %d)", op, hipGetErrorString(status), static_cast<int>(status));
-}
-int select(Plan *p, char *err, size_t cap) {
-    if (!p) return fail(1, err, cap, "null context");
-    const auto status = hipSetDevice(p->device);
-    return status == hipSuccess ? 0 : runtime_error(status, err, cap, "hipSetDevice");
-}
-bool matrix_size(uint32_t x, uint32_t y, size_t &count) {
-    const auto maximum = std::numeric_limits<size_t>::max();
-    if (!x || !y || static_cast<size_t>(x) > maximum / y) return false;
-    count = static_cast<size_t>(x) * y;
-    return count <= maximum / sizeof(float);
-}
-void cleanup(Plan *p) {
-    if (!p) return;
-    (void)hipSetDevice(p->device);
-    if (p->stream) (void)hipStreamSynchronize(p->stream);
-    if (p->start) (void)hipEventDestroy(p->start);
-    if (p->stop) (void)hipEventDestroy(p->stop);
-    if (p->a) (void)hipFree(p->a);
-    if (p->b) (void)hipFree(p->b);
-    if (p->c) (void)hipFree(p->c);
-    if (p->workspace) (void)hipFree(p->workspace);
-    if (p->stream) (void)hipStreamDestroy(p->stream);
-    delete p;
+jade::dev::HandleSet<GemmPlan> g_plans;
+
+GemmPlan &plan_of(void *handle) {
+    GemmPlan *p = g_plans.find(handle);
+    if (!p) refuse_invalid("unknown GEMM plan handle (null, destroyed, or not from jade_corex_create)");
+    return *p;
 }
 
 }  // namespace
@@ -74,152 +81,92 @@ extern "C" uint32_t jade_corex_abi_version(void) { return 1; }
 
 extern "C" int jade_corex_create(uint32_t m, uint32_t n, uint32_t k, int device, uint32_t precision, void **out,
                                  char *err, size_t cap) {
-    clear_error(err, cap);
-    if (!out) return fail(1, err, cap, "null output handle");
-    *out = nullptr;
-    if (!m || !n || !k || m > INT_MAX || n > INT_MAX || k > INT_MAX || device < 0 || precision > 1)
-        return fail(1, err, cap, "dimensions must be 1..INT_MAX; device >= 0; precision 0 or 1");
-    if (precision == 1)
-        return fail(1, err, cap, "precision 1 (FP16 inputs) is not provided by the HIP backend; use precision 0");
-    auto *p = new (std::nothrow) Plan();
-    if (!p) return fail(4, err, cap, "context allocation failed");
-    p->m = int(m);
-    p->n = int(n);
-    p->k = int(k);
-    p->device = device;
-    if (!matrix_size(m, k, p->a_len) || !matrix_size(k, n, p->b_len) || !matrix_size(m, n, p->c_len) ||
-        p->a_len > size_t(INT_MAX) || p->b_len > size_t(INT_MAX) || p->c_len > size_t(INT_MAX)) {
-        delete p;
-        return fail(1, err, cap, "each matrix must hold at most INT_MAX elements");
-    }
-    const auto initialize = [&]() -> int {
-        int count = 0;
-        auto status = hipGetDeviceCount(&count);
-        if (status != hipSuccess) return runtime_error(status, err, cap, "hipGetDeviceCount");
-        if (device >= count) return fail(1, err, cap, "device %d outside detected count %d", device, count);
-        int rc = select(p, err, cap);
-        if (rc) return rc;
-        status = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
-        if (status != hipSuccess) return runtime_error(status, err, cap, "hipStreamCreateWithFlags");
-        status = hipEventCreate(&p->start);
-        if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventCreate(start)");
-        status = hipEventCreate(&p->stop);
-        if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventCreate(stop)");
-        status = hipMalloc(&p->a, p->a_len * sizeof(float));
-        if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(A): %s", hipGetErrorString(status));
-        status = hipMalloc(&p->b, p->b_len * sizeof(float));
-        if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(B): %s", hipGetErrorString(status));
-        status = hipMalloc(&p->c, p->c_len * sizeof(float));
-        if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(C): %s", hipGetErrorString(status));
-        const size_t ws = jade::hipk::gemm_f32_workspace_bytes(m, n, k);
-        if (ws) {
-            status = hipMalloc(&p->workspace, ws);
-            if (status != hipSuccess) return fail(4, err, cap, "hipMalloc(workspace): %s", hipGetErrorString(status));
-        }
-        return 0;
-    };
-    const int rc = initialize();
-    if (rc) {
-        cleanup(p);
-        return rc;
-    }
-    *out = p;
-    return 0;
+    if (out) *out = nullptr;
+    return entry(err, cap, [&] {
+        if (!out) refuse_invalid("jade_corex_create needs somewhere to return the plan");
+        if (precision == 1)
+            refuse_invalid("precision 1 (FP16 operands) is not offered by the HIP backend; use precision 0 (FP32)");
+        if (precision != 0) refuse_invalid(text_of("unknown precision %u (0 = FP32)", precision));
+        if (!m || !n || !k) refuse_invalid(text_of("GEMM plan %ux%ux%u has an empty dimension", m, n, k));
+        char why[512];
+        std::unique_ptr<GemmPlan> p(new GemmPlan);
+        p->m = m;
+        p->n = n;
+        p->k = k;
+        forward(jr_create(device, &p->runtime, why, sizeof why), why);
+        const std::string spec = text_of("{\"op\":\"gemm\",\"m\":%u,\"n\":%u,\"k\":%u,\"tiled\":true}", m, n, k);
+        forward(jr_compile(p->runtime, spec.data(), spec.size(), &p->kernel, why, sizeof why), why);
+        forward(jr_alloc(p->runtime, p->a_len() * sizeof(float), &p->a, why, sizeof why), why);
+        forward(jr_alloc(p->runtime, p->b_len() * sizeof(float), &p->b, why, sizeof why), why);
+        forward(jr_alloc(p->runtime, p->c_len() * sizeof(float), &p->c, why, sizeof why), why);
+        g_plans.add(p.get());
+        *out = p.release();
+    });
 }
 
 extern "C" int jade_corex_upload(void *handle, const float *a, size_t a_len, const float *b, size_t b_len, char *err,
                                  size_t cap) {
-    clear_error(err, cap);
-    auto *p = static_cast<Plan *>(handle);
-    if (!p || !a || !b || a_len != p->a_len || b_len != p->b_len)
-        return fail(1, err, cap, "upload requires non-null buffers and exact A/B element counts");
-    p->uploaded = false;
-    p->computed = false;
-    const int rc = select(p, err, cap);
-    if (rc) return rc;
-    auto status = hipMemcpyAsync(p->a, a, a_len * sizeof(float), hipMemcpyHostToDevice, p->stream);
-    if (status == hipSuccess) status = hipMemcpyAsync(p->b, b, b_len * sizeof(float), hipMemcpyHostToDevice, p->stream);
-    const auto sync = hipStreamSynchronize(p->stream);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipMemcpyAsync(upload)");
-    if (sync != hipSuccess) return runtime_error(sync, err, cap, "hipStreamSynchronize(upload)");
-    p->uploaded = true;
-    return 0;
+    return entry(err, cap, [&] {
+        GemmPlan &p = plan_of(handle);
+        if (!a || !b) refuse_invalid("upload needs both host operands");
+        if (a_len != p.a_len() || b_len != p.b_len())
+            refuse_invalid(text_of("upload of a %ux%ux%u plan takes exactly %zu A and %zu B elements (got %zu, %zu)",
+                                   p.m, p.n, p.k, p.a_len(), p.b_len(), a_len, b_len));
+        p.holds = GemmPlan::Holds::Nothing;
+        char why[512];
+        forward(jr_upload(p.runtime, p.a, a, a_len * sizeof(float), why, sizeof why), why);
+        forward(jr_upload(p.runtime, p.b, b, b_len * sizeof(float), why, sizeof why), why);
+        p.holds = GemmPlan::Holds::Operands;
+    });
 }
 
 extern "C" int jade_corex_run(void *handle, uint32_t iterations, double *elapsed_ms, char *err, size_t cap) {
-    clear_error(err, cap);
     if (elapsed_ms) *elapsed_ms = 0;
-    auto *p = static_cast<Plan *>(handle);
-    if (!p || !iterations || !elapsed_ms)
-        return fail(1, err, cap, "run requires context, iterations > 0 and elapsed output");
-    p->computed = false;
-    if (!p->uploaded) return fail(1, err, cap, "upload A/B before running");
-    const int rc = select(p, err, cap);
-    if (rc) return rc;
-    auto status = hipEventRecord(p->start, p->stream);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventRecord(start)");
-    for (uint32_t i = 0; i < iterations; ++i) {
-        status = jade::hipk::gemm_f32(p->stream, p->a, p->b, p->c, uint32_t(p->m), uint32_t(p->n), uint32_t(p->k),
-                                      p->workspace);
-        if (status != hipSuccess) {
-            (void)hipStreamSynchronize(p->stream);
-            return runtime_error(status, err, cap, "matrix multiplication");
-        }
-    }
-    status = hipEventRecord(p->stop, p->stream);
-    if (status != hipSuccess) {
-        (void)hipStreamSynchronize(p->stream);
-        return runtime_error(status, err, cap, "hipEventRecord(stop)");
-    }
-    status = hipEventSynchronize(p->stop);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventSynchronize");
-    float milliseconds = 0;
-    status = hipEventElapsedTime(&milliseconds, p->start, p->stop);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipEventElapsedTime");
-    if (!std::isfinite(milliseconds) || milliseconds < 0) return fail(2, err, cap, "invalid GPU event duration");
-    *elapsed_ms = static_cast<double>(milliseconds);
-    p->computed = true;
-    return 0;
+    return entry(err, cap, [&] {
+        GemmPlan &p = plan_of(handle);
+        if (!iterations) refuse_invalid("run needs at least one iteration");
+        if (!elapsed_ms) refuse_invalid("run needs somewhere to write the elapsed milliseconds");
+        if (p.holds == GemmPlan::Holds::Nothing) refuse_invalid("nothing to multiply: upload A and B first");
+        void *buffers[3] = {p.a, p.b, p.c};
+        const jr_dispatch job{p.kernel, buffers, 3};
+        p.holds = GemmPlan::Holds::Operands;  // C is undefined until this run succeeds
+        char why[512];
+        forward(jr_execute_dispatches(p.runtime, &job, 1, iterations, elapsed_ms, why, sizeof why), why);
+        p.holds = GemmPlan::Holds::Product;
+    });
 }
 
 extern "C" int jade_corex_download(void *handle, float *out, size_t out_len, char *err, size_t cap) {
-    clear_error(err, cap);
-    auto *p = static_cast<Plan *>(handle);
-    if (!p || !out || out_len != p->c_len) return fail(1, err, cap, "download requires exact C element count");
-    if (!p->computed) return fail(1, err, cap, "run successfully before downloading C");
-    const int rc = select(p, err, cap);
-    if (rc) return rc;
-    const auto status = hipMemcpyAsync(out, p->c, p->c_len * sizeof(float), hipMemcpyDeviceToHost, p->stream);
-    const auto sync = hipStreamSynchronize(p->stream);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipMemcpyAsync(download)");
-    return sync == hipSuccess ? 0 : runtime_error(sync, err, cap, "hipStreamSynchronize(download)");
+    return entry(err, cap, [&] {
+        GemmPlan &p = plan_of(handle);
+        if (!out) refuse_invalid("download needs a host destination");
+        if (out_len != p.c_len())
+            refuse_invalid(text_of("C of a %ux%ux%u plan holds %zu elements, not %zu", p.m, p.n, p.k, p.c_len(),
+                                   out_len));
+        if (p.holds != GemmPlan::Holds::Product) refuse_invalid("no product yet: a run must succeed before download");
+        char why[512];
+        forward(jr_download(p.runtime, p.c, out, out_len * sizeof(float), why, sizeof why), why);
+    });
 }
 
 extern "C" int jade_corex_device_info(void *handle, char *out, size_t out_cap, char *err, size_t cap) {
-    clear_error(err, cap);
     if (out && out_cap) out[0] = '\0';
-    auto *p = static_cast<Plan *>(handle);
-    if (!p || !out || !out_cap) return fail(1, err, cap, "device info requires context and output buffer");
-    const int rc = select(p, err, cap);
-    if (rc) return rc;
-    hipDeviceProp_t prop{};
-    auto status = hipGetDeviceProperties(&prop, p->device);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipGetDeviceProperties");
-    int runtime = 0, driver = 0;
-    status = hipRuntimeGetVersion(&runtime);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipRuntimeGetVersion");
-    status = hipDriverGetVersion(&driver);
-    if (status != hipSuccess) return runtime_error(status, err, cap, "hipDriverGetVersion");
-    const int needed = std::snprintf(out, out_cap,
-                                     "device=%d name=%.255s memory_bytes=%llu multiprocessors=%d runtime_api=%d "
-                                     "driver_api=%d blas_api=0 precision=fp32 arch=%.63s gemm=jade_mfma_f32",
-                                     p->device, prop.name, static_cast<unsigned long long>(prop.totalGlobalMem),
-                                     prop.multiProcessorCount, runtime, driver, prop.gcnArchName);
-    if (needed < 0 || static_cast<size_t>(needed) >= out_cap) {
-        out[out_cap - 1] = '\0';
-        return fail(1, err, cap, "device info output buffer too small");
-    }
-    return 0;
+    return entry(err, cap, [&] {
+        GemmPlan &p = plan_of(handle);
+        if (!out || !out_cap) refuse_invalid("device info needs an output buffer");
+        char device[768];
+        char why[512];
+        forward(jr_info(p.runtime, device, sizeof device, why, sizeof why), why);
+        const std::string text =
+            text_of("%s gemm=jade_mfma_f32 precision=fp32 plan=%ux%ux%u", device, p.m, p.n, p.k);
+        if (text.size() + 1 > out_cap)
+            refuse_invalid(text_of("output buffer holds %zu bytes; the device info needs %zu", out_cap,
+                                   text.size() + 1));
+        jade::dev::copy_text(text, out, out_cap);
+    });
 }
 
-extern "C" void jade_corex_destroy(void *handle) { cleanup(static_cast<Plan *>(handle)); }
+extern "C" void jade_corex_destroy(void *handle) {
+    GemmPlan *p = g_plans.find(handle);
+    if (p && g_plans.remove(p)) delete p;
+}

@@ -1,563 +1,89 @@
-// jr_* ABI 2 for gfx950: the device layer of the reference's native runtime
-// (native/jade_runtime_corex.cpp:1-189) plus the checks its Rust CoreX backend
-// did before calling it (src/runtime/corex.rs:322-612), re-designed around
-// precompiled HIP kernels instead of runtime-compiled modules.
+// The jr_* C ABI of libjade_runtime_hip.so (ABI 2: the reference's
+// native/jade_runtime_corex.h:9-31 entry points plus precompiled kernels from
+// a KernelSpec). Each handle is a RuntimeContext: one dev::Session (device,
+// queue, event clock, region table) and the session's pipeline cache. Every
+// entry point is a short body run under dev::abi_entry, which maps the
+// failure kinds onto this ABI's codes: 1 invalid, 2 device, 3 memory.
+//
+// The Rust CoreX backend made its ownership, exact-length and alias checks
+// before calling into C (src/runtime/corex.rs:322-332, 389-394, 556-569); here
+// the C layer makes them itself, from the session's region table, for every
+// caller.
 #include <hip/hip_runtime.h>
 
-#include <cmath>
-#include <cstdarg>
-#include <cstdio>
-#include <cstring>
-#include <mutex>
-#include <new>
+#include <memory>
 #include <string>
-#include <unordered_map>
-#include <unordered_set>
 #include <vector>
 
 #include "jade_runtime_hip.h"
 #include "kernels.hpp"
+#include "pipeline.hpp"
+#include "session.hpp"
 #include "spec.hpp"
 
 namespace {
 
-using jade::Binding;
 using jade::KernelSpec;
 using jade::Op;
+using jade::Pipeline;
+using jade::dev::Kind;
+using jade::dev::refuse_invalid;
+using jade::dev::text_of;
 
-struct Context;
+int jr_code(Kind kind) {
+    switch (kind) {
+        case Kind::Invalid: return 1;
+        case Kind::Device: return 2;
+        case Kind::Memory: return 3;
+    }
+    return 2;
+}
 
-// A compiled pipeline: a validated spec bound to one precompiled kernel.
-struct Pipeline {
-    Context *owner = nullptr;
-    KernelSpec spec;
-    std::string canonical;
-    std::vector<Binding> binds;
-    jade::Instr *program = nullptr;  // device copy of an Elementwise program
-    uint32_t program_len = 0;
-    float *workspace = nullptr;      // split-K / split-key partials of a small GEMM or attention grid
-    bool copy = false;  // Elementwise whose expression is input0
-    int refs = 0;
+template <class Body>
+int entry(char *err, size_t cap, Body &&body) {
+    return jade::dev::abi_entry(err, cap, jr_code, body);
+}
+
+struct RuntimeContext {
+    explicit RuntimeContext(int ordinal) : session(ordinal), pipelines(session) {}
+    jade::dev::Session session;       // destroyed last: frees the regions and the queue
+    jade::PipelineCache pipelines;    // destroyed first: frees programs and workspaces
 };
 
-struct Allocation {
-    size_t bytes;
-    uint64_t id;
-};
+jade::dev::HandleSet<RuntimeContext> g_contexts;
 
-struct Context {
-    int device = 0;
-    hipStream_t stream = nullptr;
-    hipEvent_t start = nullptr, stop = nullptr;
-    std::unordered_map<const void *, Allocation> allocations;
-    std::unordered_map<std::string, Pipeline *> cache;
-    std::unordered_set<Pipeline *> pipelines;
-    uint64_t next_id = 1;
-};
-
-std::mutex g_registry_mutex;
-std::unordered_set<Context *> g_contexts;
-
-Context *lookup(void *handle) {
-    std::lock_guard<std::mutex> lock(g_registry_mutex);
-    auto *ctx = static_cast<Context *>(handle);
-    return g_contexts.count(ctx) ? ctx : nullptr;
+RuntimeContext &context_of(void *handle) {
+    RuntimeContext *c = g_contexts.find(handle);
+    if (!c) refuse_invalid("unknown runtime context handle (null, destroyed, or not from jr_create)");
+    return *c;
 }
 
-int fail(int code, char *err, size_t cap, const char *format, ...) {
-    if (err && cap) {
-        va_list args;
-        va_start(args, format);
-        std::vsnprintf(err, cap, format, args);
-        va_end(args);
-        err[cap - 1] = '\0';
-    }
-    return code;
-}
-void clear(char *err, size_t cap) {
-    if (err && cap) err[0] = '\0';
-}
-int hip_fail(hipError_t status, char *err, size_t cap, const char *operation) {
-    return fail(2, err, cap, "%s: %s (%d)", operation, hipGetErrorString(status), static_cast<int>(status));
-}
-int select(Context *ctx, char *err, size_t cap) {
-    if (!ctx) return fail(1, err, cap, "null or unknown runtime context");
-    const auto status = hipSetDevice(ctx->device);
-    return status == hipSuccess ? 0 : hip_fail(status, err, cap, "hipSetDevice");
+Pipeline &pipeline_of(RuntimeContext &c, void *kernel, const char *where) {
+    if (!kernel || !c.pipelines.holds(kernel))
+        refuse_invalid(text_of("%s: the kernel handle was not compiled by this context", where));
+    return *static_cast<Pipeline *>(kernel);
 }
 
-void release_pipeline(Context *ctx, Pipeline *p) {
-    if (p->program) (void)hipFree(p->program);
-    if (p->workspace) (void)hipFree(p->workspace);
-    ctx->cache.erase(p->canonical);
-    ctx->pipelines.erase(p);
-    delete p;
+void emit(const std::string &text, char *out, size_t out_cap) {
+    if (text.size() + 1 > out_cap)
+        refuse_invalid(text_of("output buffer holds %zu bytes; the text needs %zu", out_cap, text.size() + 1));
+    jade::dev::copy_text(text, out, out_cap);
 }
 
-void destroy(Context *ctx) {
-    if (!ctx) return;
-    (void)hipSetDevice(ctx->device);
-    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (Pipeline *p : std::vector<Pipeline *>(ctx->pipelines.begin(), ctx->pipelines.end())) release_pipeline(ctx, p);
-    for (auto &a : ctx->allocations) (void)hipFree(const_cast<void *>(a.first));
-    ctx->allocations.clear();
-    if (ctx->start) (void)hipEventDestroy(ctx->start);
-    if (ctx->stop) (void)hipEventDestroy(ctx->stop);
-    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
-    delete ctx;
-}
+// ---- batch planning for jr_execute_dispatches -----------------------------
 
-jade::hipk::LaunchShape launch_shape(const KernelSpec &s) {
-    using namespace jade::hipk;
-    switch (s.op) {
-        case Op::Elementwise: {
-            const auto &e = *s.expression;
-            if (e.kind == jade::Expr::Kind::Input && e.binding == 0) {
-                auto shape = stream_shape(s.len);
-                shape.kernel = "copy_stream";
-                return shape;
-            }
-            return elementwise_shape(s.len);
-        }
-        case Op::Axpy:
-        case Op::Add:
-        case Op::SwiGlu: return stream_shape(s.len);
-        case Op::Gemm:
-        case Op::GemmSimd: return gemm_f32_shape(s.m, s.n, s.k);
-        case Op::AttentionOnline: return attention_online_shape(s.heads, s.seq, s.dim, s.causal);
-        case Op::AttentionScores: return attention_scores_shape(s.heads, s.seq, s.dim, s.causal);
-        case Op::AttentionApply: return attention_apply_shape(s.heads, s.seq, s.dim);
-        case Op::RmsNorm: return rms_norm_shape(s.rows, s.cols);
-        case Op::Softmax: return softmax_shape(s.rows, s.cols);
-        case Op::GemmMps: break;
-    }
-    return {nullptr, {0, 0, 0}, {0, 0, 0}, 0};
-}
+const KernelSpec &spec_of(const jr_dispatch &d) { return static_cast<Pipeline *>(d.kernel)->spec; }
 
-hipError_t launch(const Pipeline &p, hipStream_t st, void *const *b) {
-    using namespace jade::hipk;
-    const KernelSpec &s = p.spec;
-    auto in = [&](size_t i) { return static_cast<const float *>(b[i]); };
-    auto out = [&](size_t i) { return static_cast<float *>(b[i]); };
-    switch (s.op) {
-        case Op::Elementwise: {
-            if (p.copy) return copy_f32(st, in(0), out(s.inputs), s.len);
-            const float *inputs[jade::kMaxElementwiseInputs] = {};
-            for (uint32_t i = 0; i < s.inputs; ++i) inputs[i] = in(i);
-            return elementwise_f32(st, inputs, s.inputs, out(s.inputs), s.len, p.program, p.program_len);
-        }
-        case Op::Axpy: return axpy_f32(st, s.alpha, in(0), in(1), out(2), s.len);
-        case Op::Add: return add_f32(st, in(0), in(1), out(2), s.len);
-        case Op::SwiGlu: return swiglu_f32(st, in(0), in(1), out(2), s.len);
-        case Op::Gemm:
-        case Op::GemmSimd: return gemm_f32(st, in(0), in(1), out(2), s.m, s.n, s.k, p.workspace);
-        case Op::AttentionOnline:
-            return attention_online_f32(st, in(0), in(1), in(2), out(3), s.heads, s.seq, s.dim, s.causal,
-                                        p.workspace);
-        case Op::AttentionScores:
-            return attention_scores_f32(st, in(0), in(1), out(2), s.heads, s.seq, s.dim, s.causal);
-        case Op::AttentionApply: return attention_apply_f32(st, in(0), in(1), out(2), s.heads, s.seq, s.dim);
-        case Op::RmsNorm: return rms_norm_f32(st, in(0), in(1), out(2), s.rows, s.cols, s.epsilon);
-        case Op::Softmax: return softmax_f32(st, in(0), out(1), s.rows, s.cols);
-        case Op::GemmMps: break;
-    }
-    return hipErrorInvalidValue;
-}
-
-// Device workspace a pipeline allocates at jr_compile (split-K partial
-// products of small GEMM grids, split-key partial rows of small attention
-// grids); 0 for every other launch.
-size_t workspace_bytes_for(const KernelSpec &spec) {
-    if (spec.op == Op::Gemm || spec.op == Op::GemmSimd)
-        return jade::hipk::gemm_f32_workspace_bytes(spec.m, spec.n, spec.k);
-    if (spec.op == Op::AttentionOnline)
-        return jade::hipk::attention_online_workspace_bytes(spec.heads, spec.seq, spec.dim, spec.causal);
-    return 0;
-}
-
-std::string describe(const KernelSpec &spec) {
-    std::string ref_error, hip_error;
-    const bool reference_valid = jade::validate(spec, jade::Rules::Reference, ref_error);
-    const bool supported = jade::hip_supported(spec, hip_error);
-    std::string out = "{\"name\":" + jade::json::quote(jade::spec_name(spec)) +
-                      ",\"spec\":" + jade::canonical_json(spec) + ",\"bindings\":[";
-    const auto binds = jade::bindings(spec);
-    for (size_t i = 0; i < binds.size(); ++i) {
-        if (i) out += ",";
-        out += "{\"name\":" + jade::json::quote(binds[i].name) +
-               ",\"elements\":" + std::to_string(binds[i].elements) +
-               ",\"write\":" + (binds[i].write ? "true" : "false") + "}";
-    }
-    out += std::string("],\"reference_valid\":") + (reference_valid ? "true" : "false");
-    out += ",\"reference_error\":" + (reference_valid ? std::string("null") : jade::json::quote(ref_error));
-    out += std::string(",\"hip_supported\":") + (supported ? "true" : "false");
-    out += ",\"hip_error\":" + (supported ? std::string("null") : jade::json::quote(hip_error));
-    if (supported) {
-        const auto shape = launch_shape(spec);
-        out += ",\"launch\":{\"kernel\":" + jade::json::quote(shape.kernel) + ",\"grid\":[" +
-               std::to_string(shape.grid[0]) + "," + std::to_string(shape.grid[1]) + "," +
-               std::to_string(shape.grid[2]) + "],\"block\":[" + std::to_string(shape.block[0]) + "," +
-               std::to_string(shape.block[1]) + "," + std::to_string(shape.block[2]) +
-               "],\"lds_bytes\":" + std::to_string(shape.lds_bytes) + "}";
-        out += ",\"workspace_bytes\":" + std::to_string(workspace_bytes_for(spec));
-    } else {
-        out += ",\"launch\":null,\"workspace_bytes\":0";
-    }
-    return out + "}";
-}
-
-int write_text(const std::string &text, char *out, size_t out_cap, char *err, size_t cap) {
-    if (text.size() + 1 > out_cap) {
-        out[out_cap - 1] = '\0';
-        return fail(1, err, cap, "description output buffer too small (%zu bytes needed)", text.size() + 1);
-    }
-    std::memcpy(out, text.c_str(), text.size() + 1);
-    return 0;
-}
-
-int parse_checked(const char *spec_json, size_t len, KernelSpec &spec, char *err, size_t cap) {
-    if (!spec_json || !len) return fail(1, err, cap, "empty kernel spec");
-    std::string error;
-    if (!jade::parse_spec(std::string(spec_json, len), spec, error))
-        return fail(1, err, cap, "kernel spec: %s", error.c_str());
-    if (!jade::validate(spec, jade::Rules::Hip, error))
-        return fail(1, err, cap, "%s: %s", jade::spec_name(spec), error.c_str());
-    return 0;
-}
-
-}  // namespace
-
-extern "C" uint32_t jr_version(void) { return 2; }
-
-extern "C" int jr_create(int device, void **out, char *err, size_t cap) {
-    clear(err, cap);
-    if (!out) return fail(1, err, cap, "null output handle");
-    *out = nullptr;
-    if (device < 0) return fail(1, err, cap, "negative device index");
-    int count = 0;
-    auto status = hipGetDeviceCount(&count);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "hipGetDeviceCount");
-    if (device >= count) return fail(1, err, cap, "device %d outside device count %d", device, count);
-    auto *ctx = new (std::nothrow) Context;
-    if (!ctx) return fail(3, err, cap, "runtime context allocation failed");
-    ctx->device = device;
-    int rc = select(ctx, err, cap);
-    if (rc) {
-        destroy(ctx);
-        return rc;
-    }
-    status = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
-    if (status == hipSuccess) status = hipEventCreate(&ctx->start);
-    if (status == hipSuccess) status = hipEventCreate(&ctx->stop);
-    if (status != hipSuccess) {
-        rc = hip_fail(status, err, cap, "create stream/timing events");
-        destroy(ctx);
-        return rc;
-    }
-    {
-        std::lock_guard<std::mutex> lock(g_registry_mutex);
-        g_contexts.insert(ctx);
-    }
-    *out = ctx;
-    return 0;
-}
-
-extern "C" void jr_destroy(void *handle) {
-    Context *ctx = lookup(handle);
-    if (!ctx) return;
-    {
-        std::lock_guard<std::mutex> lock(g_registry_mutex);
-        g_contexts.erase(ctx);
-    }
-    destroy(ctx);
-}
-
-extern "C" int jr_info(void *handle, char *out, size_t out_cap, char *err, size_t cap) {
-    clear(err, cap);
-    if (out && out_cap) out[0] = '\0';
-    if (!out || !out_cap) return fail(1, err, cap, "missing device-info output");
-    Context *ctx = lookup(handle);
-    const int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    hipDeviceProp_t prop{};
-    auto status = hipGetDeviceProperties(&prop, ctx->device);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "hipGetDeviceProperties");
-    int runtime = 0, driver = 0;
-    status = hipRuntimeGetVersion(&runtime);
-    if (status == hipSuccess) status = hipDriverGetVersion(&driver);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "runtime/driver version");
-    const int n = std::snprintf(out, out_cap,
-                                "device=%d name=%.255s memory_bytes=%llu runtime_api=%d driver_api=%d arch=%.63s "
-                                "compute_units=%d",
-                                ctx->device, prop.name, static_cast<unsigned long long>(prop.totalGlobalMem), runtime,
-                                driver, prop.gcnArchName, prop.multiProcessorCount);
-    if (n < 0 || static_cast<size_t>(n) >= out_cap) {
-        out[out_cap - 1] = '\0';
-        return fail(1, err, cap, "device-info output too small");
-    }
-    return 0;
-}
-
-extern "C" int jr_alloc(void *handle, size_t bytes, void **out, char *err, size_t cap) {
-    clear(err, cap);
-    if (!out) return fail(1, err, cap, "null allocation output");
-    *out = nullptr;
-    if (!bytes) return fail(1, err, cap, "allocation must be nonempty");
-    Context *ctx = lookup(handle);
-    const int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    auto status = hipMalloc(out, bytes);
-    if (status != hipSuccess) {
-        *out = nullptr;
-        const int code = status == hipErrorOutOfMemory ? 3 : 2;
-        return fail(code, err, cap, "hipMalloc(%zu): %s (%d)", bytes, hipGetErrorString(status), int(status));
-    }
-    // Public allocations contain defined zeros, even before the first upload.
-    status = hipMemsetAsync(*out, 0, bytes, ctx->stream);
-    const auto sync = hipStreamSynchronize(ctx->stream);
-    if (status != hipSuccess || sync != hipSuccess) {
-        (void)hipFree(*out);
-        *out = nullptr;
-        return hip_fail(status != hipSuccess ? status : sync, err, cap, "initialize allocation");
-    }
-    try {
-        ctx->allocations.emplace(*out, Allocation{bytes, ctx->next_id++});
-    } catch (...) {
-        (void)hipFree(*out);
-        *out = nullptr;
-        return fail(3, err, cap, "allocation registry insert failed");
-    }
-    return 0;
-}
-
-extern "C" void jr_free(void *handle, void *ptr) {
-    Context *ctx = lookup(handle);
-    if (!ctx || !ptr) return;
-    auto it = ctx->allocations.find(ptr);
-    if (it == ctx->allocations.end()) return;
-    if (hipSetDevice(ctx->device) != hipSuccess) return;
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(ptr);
-    ctx->allocations.erase(it);
-}
-
-static int transfer_check(Context *ctx, const void *device_ptr, size_t bytes, const char *what, char *err,
-                          size_t cap) {
-    auto it = ctx->allocations.find(device_ptr);
-    if (it == ctx->allocations.end())
-        return fail(1, err, cap, "%s: buffer belongs to another runtime/device context or is not live", what);
-    if (it->second.bytes != bytes)
-        return fail(1, err, cap, "%s element count must match buffer exactly (%zu bytes, buffer holds %zu)", what,
-                    bytes, it->second.bytes);
-    return 0;
-}
-
-extern "C" int jr_upload(void *handle, void *device_ptr, const void *host_ptr, size_t bytes, char *err, size_t cap) {
-    clear(err, cap);
-    if (!device_ptr || !host_ptr || !bytes) return fail(1, err, cap, "invalid upload buffers/size");
-    Context *ctx = lookup(handle);
-    int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    rc = transfer_check(ctx, device_ptr, bytes, "upload", err, cap);
-    if (rc) return rc;
-    const auto status = hipMemcpyAsync(device_ptr, host_ptr, bytes, hipMemcpyHostToDevice, ctx->stream);
-    const auto sync = hipStreamSynchronize(ctx->stream);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "upload");
-    return sync == hipSuccess ? 0 : hip_fail(sync, err, cap, "upload synchronization");
-}
-
-extern "C" int jr_download(void *handle, const void *device_ptr, void *host_ptr, size_t bytes, char *err,
-                           size_t cap) {
-    clear(err, cap);
-    if (!device_ptr || !host_ptr || !bytes) return fail(1, err, cap, "invalid download buffers/size");
-    Context *ctx = lookup(handle);
-    int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    rc = transfer_check(ctx, device_ptr, bytes, "download", err, cap);
-    if (rc) return rc;
-    const auto status = hipMemcpyAsync(host_ptr, device_ptr, bytes, hipMemcpyDeviceToHost, ctx->stream);
-    const auto sync = hipStreamSynchronize(ctx->stream);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "download");
-    return sync == hipSuccess ? 0 : hip_fail(sync, err, cap, "download synchronization");
-}
-
-extern "C" int jr_buffer_elements(void *handle, const void *device_ptr, size_t *elements, char *err, size_t cap) {
-    clear(err, cap);
-    if (!elements) return fail(1, err, cap, "null elements output");
-    *elements = 0;
-    Context *ctx = lookup(handle);
-    if (!ctx) return fail(1, err, cap, "null or unknown runtime context");
-    auto it = ctx->allocations.find(device_ptr);
-    if (it == ctx->allocations.end()) return fail(1, err, cap, "not a live allocation of this context");
-    *elements = it->second.bytes / sizeof(float);
-    return 0;
-}
-
-// Records events around `repeats` passes of `submit()`; `submit` returns a HIP status.
-template <typename Submit>
-static int timed_sequence(Context *ctx, uint32_t repeats, double *gpu_ms, Submit submit, char *err, size_t cap) {
-    auto status = hipEventRecord(ctx->start, ctx->stream);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "record start event");
-    for (uint32_t repeat = 0; repeat < repeats; ++repeat) {
-        status = submit();
-        if (status != hipSuccess) {
-            (void)hipStreamSynchronize(ctx->stream);
-            return hip_fail(status, err, cap, "kernel launch");
-        }
-    }
-    status = hipEventRecord(ctx->stop, ctx->stream);
-    if (status != hipSuccess) {
-        (void)hipStreamSynchronize(ctx->stream);
-        return hip_fail(status, err, cap, "record stop event");
-    }
-    status = hipEventSynchronize(ctx->stop);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "kernel synchronization");
-    float elapsed = 0;
-    status = hipEventElapsedTime(&elapsed, ctx->start, ctx->stop);
-    if (status != hipSuccess) return hip_fail(status, err, cap, "event elapsed time");
-    if (!std::isfinite(elapsed) || elapsed < 0) return fail(2, err, cap, "invalid GPU-event duration");
-    *gpu_ms = static_cast<double>(elapsed);
-    return 0;
-}
-
-extern "C" int jr_execute(void *handle, const jr_job *jobs, size_t job_count, uint32_t repeats, double *gpu_ms,
-                          char *err, size_t cap) {
-    clear(err, cap);
-    if (gpu_ms) *gpu_ms = 0;
-    if (!jobs || !job_count || !repeats || !gpu_ms)
-        return fail(1, err, cap, "empty dispatch sequence or missing timing output");
-    for (size_t j = 0; j < job_count; ++j) {
-        if (!jobs[j].launch || !jobs[j].buffers || !jobs[j].buffer_count) return fail(1, err, cap, "invalid job %zu", j);
-        for (size_t b = 0; b < jobs[j].buffer_count; ++b)
-            if (!jobs[j].buffers[b]) return fail(1, err, cap, "null buffer in job %zu", j);
-    }
-    Context *ctx = lookup(handle);
-    const int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    return timed_sequence(
-        ctx, repeats, gpu_ms,
-        [&]() -> hipError_t {
-            for (size_t j = 0; j < job_count; ++j) {
-                const int status = jobs[j].launch(static_cast<void *>(ctx->stream), jobs[j].buffers);
-                if (status != 0) return static_cast<hipError_t>(status);
-            }
-            return hipSuccess;
-        },
-        err, cap);
-}
-
-extern "C" int jr_spec_describe(const char *spec_json, size_t len, char *out, size_t out_cap, char *err,
-                                size_t cap) {
-    clear(err, cap);
-    if (out && out_cap) out[0] = '\0';
-    if (!out || !out_cap) return fail(1, err, cap, "missing description output");
-    KernelSpec spec;
-    const int rc = parse_checked(spec_json, len, spec, err, cap);
-    if (rc) return rc;
-    return write_text(describe(spec), out, out_cap, err, cap);
-}
-
-extern "C" int jr_spec_validate_bindings(const char *spec_json, size_t len, const uint64_t *lengths,
-                                         const uint64_t *ids, size_t count, char *err, size_t cap) {
-    clear(err, cap);
-    if ((!lengths || !ids) && count) return fail(1, err, cap, "null binding arrays");
-    KernelSpec spec;
-    const int rc = parse_checked(spec_json, len, spec, err, cap);
-    if (rc) return rc;
-    std::string error;
-    if (!jade::validate_bindings(spec, lengths, ids, count, error)) return fail(1, err, cap, "%s", error.c_str());
-    return 0;
-}
-
-extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void **kernel, char *err, size_t cap) {
-    clear(err, cap);
-    if (!kernel) return fail(1, err, cap, "null kernel output");
-    *kernel = nullptr;
-    Context *ctx = lookup(handle);
-    int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    KernelSpec spec;
-    rc = parse_checked(spec_json, len, spec, err, cap);
-    if (rc) return rc;
-    std::string error;
-    if (!jade::hip_supported(spec, error)) return fail(1, err, cap, "%s", error.c_str());
-    const std::string canonical = jade::canonical_json(spec);
-    auto hit = ctx->cache.find(canonical);
-    if (hit != ctx->cache.end()) {
-        hit->second->refs += 1;
-        *kernel = hit->second;
-        return 0;
-    }
-    auto *p = new (std::nothrow) Pipeline;
-    if (!p) return fail(3, err, cap, "pipeline allocation failed");
-    p->owner = ctx;
-    p->spec = spec;
-    p->canonical = canonical;
-    p->binds = jade::bindings(spec);
-    if (spec.op == Op::Elementwise) {
-        const auto code = jade::compile_expression(*spec.expression);
-        p->copy = code.size() == 1 && code[0].op == uint32_t(jade::Opcode::Input) && code[0].arg == 0;
-        p->program_len = uint32_t(code.size());
-        auto status = hipMalloc(&p->program, code.size() * sizeof(jade::Instr));
-        if (status == hipSuccess)
-            status = hipMemcpyAsync(p->program, code.data(), code.size() * sizeof(jade::Instr), hipMemcpyHostToDevice,
-                                    ctx->stream);
-        const auto sync = hipStreamSynchronize(ctx->stream);
-        if (status != hipSuccess || sync != hipSuccess) {
-            if (p->program) (void)hipFree(p->program);
-            delete p;
-            return hip_fail(status != hipSuccess ? status : sync, err, cap, "upload expression program");
-        }
-    }
-    const size_t workspace_bytes = workspace_bytes_for(spec);
-    if (workspace_bytes) {
-        const auto status = hipMalloc(&p->workspace, workspace_bytes);
-        if (status != hipSuccess) {
-            p->workspace = nullptr;
-            delete p;
-            return fail(status == hipErrorOutOfMemory ? 3 : 2, err, cap, "kernel workspace (%zu bytes): %s",
-                        workspace_bytes, hipGetErrorString(status));
-        }
-    }
-    p->refs = 1;
-    ctx->cache.emplace(canonical, p);
-    ctx->pipelines.insert(p);
-    *kernel = p;
-    return 0;
-}
-
-extern "C" void jr_kernel_release(void *handle, void *kernel) {
-    Context *ctx = lookup(handle);
-    if (!ctx || !kernel) return;
-    auto *p = static_cast<Pipeline *>(kernel);
-    if (!ctx->pipelines.count(p)) return;
-    if (--p->refs > 0) return;
-    (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
-    release_pipeline(ctx, p);
-}
-
-extern "C" int jr_kernel_describe(void *handle, void *kernel, char *out, size_t out_cap, char *err, size_t cap) {
-    clear(err, cap);
-    if (out && out_cap) out[0] = '\0';
-    if (!out || !out_cap) return fail(1, err, cap, "missing description output");
-    Context *ctx = lookup(handle);
-    if (!ctx) return fail(1, err, cap, "null or unknown runtime context");
-    auto *p = static_cast<Pipeline *>(kernel);
-    if (!kernel || !ctx->pipelines.count(p)) return fail(1, err, cap, "kernel belongs to another runtime/device context");
-    return write_text(describe(p->spec), out, out_cap, err, cap);
-}
+bool is_gemm(const KernelSpec &s) { return s.op == Op::Gemm || s.op == Op::GemmSimd; }
 
 // Two consecutive jobs run as one paired GEMM launch when both are GEMMs of
 // the same shape whose plan pairs, and neither touches the other's output:
 // job y must not read or write x's C (read-after-write, write-after-write) and
 // x must not read y's C (write-after-read). Each output is then bit-identical
 // to ordered launches.
-static bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
-    const KernelSpec &a = static_cast<Pipeline *>(x.kernel)->spec;
-    const KernelSpec &b = static_cast<Pipeline *>(y.kernel)->spec;
-    auto gemm = [](const KernelSpec &s) { return s.op == Op::Gemm || s.op == Op::GemmSimd; };
-    if (!gemm(a) || !gemm(b) || a.m != b.m || a.n != b.n || a.k != b.k) return false;
+bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
+    const KernelSpec &a = spec_of(x), &b = spec_of(y);
+    if (!is_gemm(a) || !is_gemm(b) || a.m != b.m || a.n != b.n || a.k != b.k) return false;
     if (x.buffer_count != 3 || y.buffer_count != 3) return false;
     if (!jade::hipk::gemm_f32_pairable(a.m, a.n, a.k)) return false;
     for (int i = 0; i < 3; ++i)
@@ -565,99 +91,243 @@ static bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
     return true;
 }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 // Three consecutive jobs run as one fused launch when they are the residual
 // MLP's gate and up projections and their SwiGLU (src/runtime/workloads.rs:
 // 440-465): two pairable GEMMs on the same A, then swi_glu(x's C, y's C -> D)
 // over m*n elements, with D none of the GEMMs' inputs, a shape whose plan is
 // whole 128x64 tiles and 16-byte aligned inputs. The three outputs are
 // bit-identical to the ordered launches (gemm_f32_dual_swiglu).
-static bool fusable_gate_up_swiglu(const jr_dispatch &x, const jr_dispatch &y, const jr_dispatch &z) {
+bool fusable_gate_up_swiglu(const jr_dispatch &x, const jr_dispatch &y, const jr_dispatch &z) {
     if (!pairable(x, y) || z.buffer_count != 3) return false;
-    const KernelSpec &g = static_cast<Pipeline *>(x.kernel)->spec;
-    const KernelSpec &f = static_cast<Pipeline *>(z.kernel)->spec;
+    const KernelSpec &g = spec_of(x), &f = spec_of(z);
     if (f.op != Op::SwiGlu || uint64_t(f.len) != uint64_t(g.m) * g.n) return false;
     if (x.buffers[0] != y.buffers[0] || z.buffers[0] != x.buffers[2] || z.buffers[1] != y.buffers[2]) return false;
     void *const d = z.buffers[2];
     if (d == x.buffers[0] || d == x.buffers[1] || d == y.buffers[1]) return false;
-    const uintptr_t bits = reinterpret_cast<uintptr_t>(x.buffers[0]) | reinterpret_cast<uintptr_t>(x.buffers[1]) |
-                           reinterpret_cast<uintptr_t>(y.buffers[1]);
-    return (bits & 15u) == 0 && jade::hipk::gemm_f32_dual_swiglu_fits(g.m, g.n, g.k);
+    return aligned16(x.buffers[0]) && aligned16(x.buffers[1]) && aligned16(y.buffers[1]) &&
+           jade::hipk::gemm_f32_dual_swiglu_fits(g.m, g.n, g.k);
+}
+
+// One launch of the batch: job `first` alone, or it and the one or two jobs
+// after it as one paired or fused launch.
+struct Step {
+    enum class Form { Single, Pair, GateUpSwiglu } form;
+    size_t first;
+};
+
+std::vector<Step> plan_steps(const jr_dispatch *jobs, size_t n) {
+    std::vector<Step> steps;
+    for (size_t j = 0; j < n;) {
+        if (j + 2 < n && fusable_gate_up_swiglu(jobs[j], jobs[j + 1], jobs[j + 2])) {
+            steps.push_back({Step::Form::GateUpSwiglu, j});
+            j += 3;
+        } else if (j + 1 < n && pairable(jobs[j], jobs[j + 1])) {
+            steps.push_back({Step::Form::Pair, j});
+            j += 2;
+        } else {
+            steps.push_back({Step::Form::Single, j});
+            j += 1;
+        }
+    }
+    return steps;
+}
+
+hipError_t run_step(const Step &step, const jr_dispatch *jobs, hipStream_t q) {
+    const jr_dispatch &x = jobs[step.first];
+    auto f = [](void *p) { return static_cast<float *>(p); };
+    auto cf = [](void *p) { return static_cast<const float *>(p); };
+    switch (step.form) {
+        case Step::Form::Single: return jade::enqueue(*static_cast<Pipeline *>(x.kernel), q, x.buffers);
+        case Step::Form::Pair: {
+            const KernelSpec &s = spec_of(x);
+            const jr_dispatch &y = jobs[step.first + 1];
+            return jade::hipk::gemm_f32_pair(q, cf(x.buffers[0]), cf(x.buffers[1]), f(x.buffers[2]),
+                                             cf(y.buffers[0]), cf(y.buffers[1]), f(y.buffers[2]), s.m, s.n, s.k);
+        }
+        case Step::Form::GateUpSwiglu: {
+            const KernelSpec &s = spec_of(x);
+            const jr_dispatch &y = jobs[step.first + 1];
+            const jr_dispatch &z = jobs[step.first + 2];
+            return jade::hipk::gemm_f32_dual_swiglu(q, cf(x.buffers[0]), cf(x.buffers[1]), cf(y.buffers[1]),
+                                                    f(x.buffers[2]), f(y.buffers[2]), f(z.buffers[2]), s.m, s.n,
+                                                    s.k);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+void check_batch(const void *jobs, size_t job_count, uint32_t repeats, const double *gpu_ms) {
+    if (!jobs || !job_count) refuse_invalid("the batch holds no jobs");
+    if (!repeats) refuse_invalid("repeats must be at least 1");
+    if (!gpu_ms) refuse_invalid("no place to write the measured milliseconds");
+}
+
+}  // namespace
+
+extern "C" uint32_t jr_version(void) { return 2; }
+
+extern "C" int jr_create(int device, void **out, char *err, size_t cap) {
+    if (out) *out = nullptr;
+    return entry(err, cap, [&] {
+        if (!out) refuse_invalid("jr_create needs somewhere to return the handle");
+        std::unique_ptr<RuntimeContext> c(new RuntimeContext(device));
+        g_contexts.add(c.get());
+        *out = c.release();
+    });
+}
+
+extern "C" void jr_destroy(void *handle) {
+    RuntimeContext *c = g_contexts.find(handle);
+    if (!c || !g_contexts.remove(c)) return;
+    (void)hipSetDevice(c->session.ordinal());
+    delete c;
+}
+
+extern "C" int jr_info(void *handle, char *out, size_t out_cap, char *err, size_t cap) {
+    if (out && out_cap) out[0] = '\0';
+    return entry(err, cap, [&] {
+        if (!out || !out_cap) refuse_invalid("jr_info needs an output buffer");
+        emit(context_of(handle).session.device_summary(), out, out_cap);
+    });
+}
+
+extern "C" int jr_alloc(void *handle, size_t bytes, void **out, char *err, size_t cap) {
+    if (out) *out = nullptr;
+    return entry(err, cap, [&] {
+        if (!out) refuse_invalid("jr_alloc needs somewhere to return the pointer");
+        RuntimeContext &c = context_of(handle);
+        *out = c.session.allocate_zeroed(bytes);
+    });
+}
+
+extern "C" void jr_free(void *handle, void *ptr) {
+    RuntimeContext *c = g_contexts.find(handle);
+    if (c && ptr) (void)c->session.give_back(ptr);
+}
+
+extern "C" int jr_upload(void *handle, void *device_ptr, const void *host_ptr, size_t bytes, char *err, size_t cap) {
+    return entry(err, cap, [&] { context_of(handle).session.write_region(device_ptr, host_ptr, bytes); });
+}
+
+extern "C" int jr_download(void *handle, const void *device_ptr, void *host_ptr, size_t bytes, char *err,
+                           size_t cap) {
+    return entry(err, cap, [&] { context_of(handle).session.read_region(host_ptr, device_ptr, bytes); });
+}
+
+extern "C" int jr_buffer_elements(void *handle, const void *device_ptr, size_t *elements, char *err, size_t cap) {
+    if (elements) *elements = 0;
+    return entry(err, cap, [&] {
+        if (!elements) refuse_invalid("jr_buffer_elements needs an output");
+        const auto *r = context_of(handle).session.region(device_ptr);
+        if (!r) refuse_invalid("the pointer is not a live region of this context");
+        *elements = r->bytes / sizeof(float);
+    });
+}
+
+extern "C" int jr_execute(void *handle, const jr_job *jobs, size_t job_count, uint32_t repeats, double *gpu_ms,
+                          char *err, size_t cap) {
+    if (gpu_ms) *gpu_ms = 0;
+    return entry(err, cap, [&] {
+        check_batch(jobs, job_count, repeats, gpu_ms);
+        for (size_t j = 0; j < job_count; ++j) {
+            if (!jobs[j].launch) refuse_invalid(text_of("job %zu has no launcher", j));
+            if (!jobs[j].buffers || !jobs[j].buffer_count) refuse_invalid(text_of("job %zu binds no buffers", j));
+            for (size_t b = 0; b < jobs[j].buffer_count; ++b)
+                if (!jobs[j].buffers[b]) refuse_invalid(text_of("job %zu: buffer %zu is null", j, b));
+        }
+        RuntimeContext &c = context_of(handle);
+        c.session.make_current();
+        *gpu_ms = c.session.clocked(repeats, [&](hipStream_t q) -> hipError_t {
+            for (size_t j = 0; j < job_count; ++j) {
+                const int status = jobs[j].launch(static_cast<void *>(q), jobs[j].buffers);
+                if (status) return static_cast<hipError_t>(status);
+            }
+            return hipSuccess;
+        });
+    });
+}
+
+extern "C" int jr_spec_describe(const char *spec_json, size_t len, char *out, size_t out_cap, char *err,
+                                size_t cap) {
+    if (out && out_cap) out[0] = '\0';
+    return entry(err, cap, [&] {
+        if (!out || !out_cap) refuse_invalid("jr_spec_describe needs an output buffer");
+        emit(jade::describe_spec(jade::read_spec(spec_json, len)), out, out_cap);
+    });
+}
+
+extern "C" int jr_spec_validate_bindings(const char *spec_json, size_t len, const uint64_t *lengths,
+                                         const uint64_t *ids, size_t count, char *err, size_t cap) {
+    return entry(err, cap, [&] {
+        if ((!lengths || !ids) && count) refuse_invalid("binding lengths and identities are missing");
+        const KernelSpec spec = jade::read_spec(spec_json, len);
+        std::string error;
+        if (!jade::validate_bindings(spec, lengths, ids, count, error)) refuse_invalid(error);
+    });
+}
+
+extern "C" int jr_compile(void *handle, const char *spec_json, size_t len, void **kernel, char *err, size_t cap) {
+    if (kernel) *kernel = nullptr;
+    return entry(err, cap, [&] {
+        if (!kernel) refuse_invalid("jr_compile needs somewhere to return the kernel");
+        RuntimeContext &c = context_of(handle);
+        const KernelSpec spec = jade::read_spec(spec_json, len);
+        *kernel = c.pipelines.obtain(spec);
+    });
+}
+
+extern "C" void jr_kernel_release(void *handle, void *kernel) {
+    RuntimeContext *c = g_contexts.find(handle);
+    if (c && kernel) c->pipelines.drop(static_cast<Pipeline *>(kernel));
+}
+
+extern "C" int jr_kernel_describe(void *handle, void *kernel, char *out, size_t out_cap, char *err, size_t cap) {
+    if (out && out_cap) out[0] = '\0';
+    return entry(err, cap, [&] {
+        if (!out || !out_cap) refuse_invalid("jr_kernel_describe needs an output buffer");
+        RuntimeContext &c = context_of(handle);
+        emit(jade::describe_spec(pipeline_of(c, kernel, "jr_kernel_describe").spec), out, out_cap);
+    });
 }
 
 extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size_t job_count, uint32_t repeats,
                                      double *gpu_ms, char *err, size_t cap) {
-    clear(err, cap);
     if (gpu_ms) *gpu_ms = 0;
-    if (!jobs || !job_count || !repeats || !gpu_ms)
-        return fail(1, err, cap, "execution requires jobs, positive repeats and a timing output");
-    Context *ctx = lookup(handle);
-    if (!ctx) return fail(1, err, cap, "null or unknown runtime context");
-    // Whole-batch validation before any submission (corex.rs:556-569).
-    std::vector<uint64_t> lengths, ids;
-    for (size_t j = 0; j < job_count; ++j) {
-        auto *p = static_cast<Pipeline *>(jobs[j].kernel);
-        if (!p || !ctx->pipelines.count(p))
-            return fail(1, err, cap, "job %zu: kernel belongs to another runtime/device context", j);
-        if (!jobs[j].buffers && jobs[j].buffer_count) return fail(1, err, cap, "job %zu: null buffer array", j);
-        lengths.assign(jobs[j].buffer_count, 0);
-        ids.assign(jobs[j].buffer_count, 0);
-        for (size_t b = 0; b < jobs[j].buffer_count; ++b) {
-            auto it = ctx->allocations.find(jobs[j].buffers[b]);
-            if (!jobs[j].buffers[b] || it == ctx->allocations.end())
-                return fail(1, err, cap, "job %zu: buffer %zu belongs to another runtime/device context", j, b);
-            if (it->second.bytes % sizeof(float))
-                return fail(1, err, cap, "job %zu: buffer %zu is not a whole number of floats", j, b);
-            lengths[b] = it->second.bytes / sizeof(float);
-            ids[b] = it->second.id;
+    return entry(err, cap, [&] {
+        check_batch(jobs, job_count, repeats, gpu_ms);
+        RuntimeContext &c = context_of(handle);
+        // The whole batch is checked before anything is enqueued
+        // (corex.rs:556-569): owned kernel, owned regions, binding count,
+        // exact lengths, no write aliasing.
+        std::vector<uint64_t> lengths, ids;
+        for (size_t j = 0; j < job_count; ++j) {
+            const std::string where = text_of("job %zu", j);
+            const Pipeline &p = pipeline_of(c, jobs[j].kernel, where.c_str());
+            if (!jobs[j].buffers && jobs[j].buffer_count) refuse_invalid(where + ": null buffer list");
+            lengths.assign(jobs[j].buffer_count, 0);
+            ids.assign(jobs[j].buffer_count, 0);
+            for (size_t b = 0; b < jobs[j].buffer_count; ++b) {
+                const auto *r = c.session.region(jobs[j].buffers[b]);
+                if (!r) refuse_invalid(text_of("job %zu: buffer %zu is not a live region of this context", j, b));
+                if (r->bytes % sizeof(float))
+                    refuse_invalid(text_of("job %zu: buffer %zu is not a whole number of f32 elements", j, b));
+                lengths[b] = r->bytes / sizeof(float);
+                ids[b] = r->serial;
+            }
+            std::string error;
+            if (!jade::validate_bindings(p.spec, lengths.data(), ids.data(), jobs[j].buffer_count, error))
+                refuse_invalid(where + ": " + error);
         }
-        std::string error;
-        if (!jade::validate_bindings(p->spec, lengths.data(), ids.data(), jobs[j].buffer_count, error))
-            return fail(1, err, cap, "job %zu: %s", j, error.c_str());
-    }
-    const int rc = select(ctx, err, cap);
-    if (rc) return rc;
-    // The MLP's gate/up GEMMs and SwiGLU fuse into one launch
-    // (fusable_gate_up_swiglu()); other adjacent independent GEMMs of one
-    // shape share a launch (pairable()).
-    std::vector<bool> paired(job_count, false), fused(job_count, false);
-    for (size_t j = 0; j + 1 < job_count; ++j) {
-        if (j + 2 < job_count && fusable_gate_up_swiglu(jobs[j], jobs[j + 1], jobs[j + 2])) {
-            fused[j] = true;
-            j += 2;
-        } else if (pairable(jobs[j], jobs[j + 1])) {
-            paired[j] = true;
-            ++j;
-        }
-    }
-    return timed_sequence(
-        ctx, repeats, gpu_ms,
-        [&]() -> hipError_t {
-            for (size_t j = 0; j < job_count; ++j) {
-                hipError_t status;
-                if (fused[j]) {
-                    const KernelSpec &s = static_cast<Pipeline *>(jobs[j].kernel)->spec;
-                    void *const *x = jobs[j].buffers;
-                    void *const *y = jobs[j + 1].buffers;
-                    status = jade::hipk::gemm_f32_dual_swiglu(
-                        ctx->stream, static_cast<const float *>(x[0]), static_cast<const float *>(x[1]),
-                        static_cast<const float *>(y[1]), static_cast<float *>(x[2]), static_cast<float *>(y[2]),
-                        static_cast<float *>(jobs[j + 2].buffers[2]), s.m, s.n, s.k);
-                    j += 2;
-                } else if (paired[j]) {
-                    const KernelSpec &s = static_cast<Pipeline *>(jobs[j].kernel)->spec;
-                    void *const *x = jobs[j].buffers;
-                    void *const *y = jobs[j + 1].buffers;
-                    status = jade::hipk::gemm_f32_pair(
-                        ctx->stream, static_cast<const float *>(x[0]), static_cast<const float *>(x[1]),
-                        static_cast<float *>(x[2]), static_cast<const float *>(y[0]), static_cast<const float *>(y[1]),
-                        static_cast<float *>(y[2]), s.m, s.n, s.k);
-                    ++j;
-                } else {
-                    status = launch(*static_cast<Pipeline *>(jobs[j].kernel), ctx->stream, jobs[j].buffers);
-                }
+        const std::vector<Step> steps = plan_steps(jobs, job_count);
+        c.session.make_current();
+        *gpu_ms = c.session.clocked(repeats, [&](hipStream_t q) -> hipError_t {
+            for (const Step &s : steps) {
+                const hipError_t status = run_step(s, jobs, q);
                 if (status != hipSuccess) return status;
             }
             return hipSuccess;
-        },
-        err, cap);
+        });
+    });
 }

@@ -9,7 +9,13 @@ namespace {
 using json::Value;
 
 constexpr uint64_t kIntMax = 2147483647ull;  // i32::MAX, the reference's index bound
-constexpr uint32_t kHipMaxHeads = 65535;       // grid.y of the attention launches
+// HIP grid limits of the attention launches. Heads: grid.y of the batched
+// P.V launch and grid.z of the score launches may not exceed 65535 (the
+// online kernel puts heads on grid.x, but all attention ops share the cap).
+// Sequence: the online kernel's query blocks (at least 128 queries each) sit
+// on grid.y, so seq may not exceed 65535 * 128.
+constexpr uint32_t kHipMaxHeads = 65535;
+constexpr uint32_t kHipMaxOnlineSeq = 65535u * 128u;
 
 struct OpName {
     const char *tag;
@@ -289,6 +295,10 @@ bool validate(const KernelSpec &s, Rules rules, std::string &error) {
             const uint64_t hs = uint64_t(s.heads) * s.seq;
             if (!matrix_ok(hs, s.dim, error)) return false;
             if (s.op != Op::AttentionOnline) return matrix_ok(hs, s.seq, error);
+            if (s.seq > kHipMaxOnlineSeq) {
+                error = "online attention sequence must be at most 8388480 (65535 query blocks of 128)";
+                return false;
+            }
             return true;
         }
         case Op::RmsNorm:

@@ -280,3 +280,39 @@ def test_big_plan_covers_every_tile_once(m, n, tail_tm, tail_tn):
                 key = (tm * bm_ // 64 + i, tn * bn_ // 64 + j)
                 count[key] = count.get(key, 0) + 1
     assert len(count) == (m // 64) * (n // 64) and set(count.values()) == {1}
+
+
+ROUTE_DIMS = (1, 3, 4, 31, 32, 33, 64, 100, 127, 128, 255, 256, 500, 512, 513, 777, 1000, 1024, 2048, 4096, 8192)
+
+
+def test_every_gemm_shape_routes_to_a_launch():
+    # gemm_f32 and its description take their decision from one route
+    # (gemm_f32.hip route_for): a shape whose plan has no kernel
+    # instantiation is described as unsupported and rejected by jr_compile,
+    # never launched as nothing. Every shape of this grid (aligned and
+    # unaligned rows, edge and interior tiles, every plan family) has one.
+    seen = set()
+    shapes = [(m, n, k) for m in ROUTE_DIMS for n in ROUTE_DIMS for k in ROUTE_DIMS]
+    # Long K (register-staged 64-bit loads) and operands of 2 GiB or more
+    # with unaligned rows (clamped loads, two K groups at most).
+    shapes += [(64, 64, 8912896), (1000, 777, 2097153), (300, 700, 2097153), (8192, 8192, 8)]
+    # 256x256 whole rounds with a 64x64 or 128x128 tail.
+    shapes += [(5120, 5120, 2048), (4352, 4096, 1024)]
+    for m, n, k in shapes:
+        d = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+        assert d["hip_supported"] and d["launch"]["kernel"], (m, n, k, d["hip_error"])
+        seen.add(d["launch"]["kernel"])
+    families = {"gemm_f32_mfma_256x256x32_tail64x64", "gemm_f32_mfma_256x256x32_tail128x128", "gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x64x32",
+                "gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_k2", "gemm_f32_mfma_64x64x32_k4",
+                "gemm_f32_mfma_64x64x32_splitk_k2", "gemm_f32_direct_32x32x32_w4",
+                "gemm_f32_direct_32x32x32_w4_splitk"}
+    assert families <= seen, families - seen
+
+
+def test_online_attention_query_blocks_fit_the_grid():
+    # The online kernel's query blocks (>= 128 queries each) sit on grid.y,
+    # whose HIP limit is 65535 blocks.
+    ok = describe({"op": "attention_online", "heads": 1, "seq": 65535 * 128, "dim": 1, "causal": False})
+    assert ok["launch"]["grid"][1] <= 65535
+    msg = rejected({"op": "attention_online", "heads": 1, "seq": 65535 * 128 + 1, "dim": 1, "causal": False})
+    assert "8388480" in msg
