@@ -639,11 +639,16 @@ constexpr bool dma_offsets_fit(uint32_t bm, uint32_t bn, uint32_t k, uint32_t n)
 // pair: a second, independent product of the same shape in the same launch
 // (pair.tiles > 0): positions [tiles, 2*tiles) of the XCD order compute
 // pair.c = pair.a * pair.b.
+// pair.sum (single products only): the epilogue also stores
+// sum = C + residual elementwise (both [M, N]), the FP32 add of the stream
+// kernel, so `sum` is bit-identical to an Add launched after the product.
 struct PairArgs {
     const float *a;
     const float *b;
     float *c;
     int tiles;
+    const float *residual;
+    float *sum;
 };
 
 // KG > 1: KG groups of four waves share the workgroup's tile. Group g sums
@@ -749,7 +754,11 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (PATH == kDmaOnly || (row < M && col < N)) out[(size_t)row * N + col] = acc[i][j][v];
+                if (PATH == kDmaOnly || (row < M && col < N)) {
+                    const size_t at = size_t(row) * N + col;
+                    out[at] = acc[i][j][v];
+                    if (pair.sum) pair.sum[at] = acc[i][j][v] + pair.residual[at];
+                }
             }
         }
     }
@@ -1513,8 +1522,23 @@ hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, f
     if (!gemm_f32_pairable(m, n, k)) return hipErrorInvalidValue;
     if (!aligned16(a0) || !aligned16(b0) || !aligned16(a1) || !aligned16(b1)) return hipErrorInvalidValue;
     const Route r = route_for(m, n, k);
-    const PairArgs pair{a1, b1, c1, r.plan.tiles_m * r.plan.tiles_n};
+    const PairArgs pair{a1, b1, c1, r.plan.tiles_m * r.plan.tiles_n, nullptr, nullptr};
     return launch_route_tiles(stream, r, a0, b0, c0, m, n, k, pair);
+}
+
+bool gemm_f32_residual_fits(uint32_t m, uint32_t n, uint32_t k) {
+    const Route r = route_for(m, n, k);
+    return r.launchable && !r.plan.big && !r.plan.direct && r.plan.slices == 1;
+}
+
+hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b, float *c, const float *residual,
+                             float *sum, uint32_t m, uint32_t n, uint32_t k) {
+    if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum)
+        return hipErrorInvalidValue;
+    PairArgs extra{};
+    extra.residual = residual;
+    extra.sum = sum;
+    return launch_route_tiles(stream, route_for(m, n, k), a, b, c, m, n, k, extra);
 }
 
 bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {

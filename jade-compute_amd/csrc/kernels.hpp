@@ -40,6 +40,15 @@ hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const flo
 bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k);
 hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,
                                 float *u, float *act, uint32_t m, uint32_t n, uint32_t k);
+// C = A B and, in the same epilogue, sum = C + residual (all [m, n]): the
+// residual MLP's down projection and residual Add (src/runtime/workloads.rs:
+// 440-465) in one launch, both outputs bit-identical to gemm_f32 followed by
+// add_f32. Only where gemm_f32_residual_fits (plans of the four-wave tile
+// kernel without split K); otherwise returns hipErrorInvalidValue without
+// launching. `sum` must not alias a or b.
+bool gemm_f32_residual_fits(uint32_t m, uint32_t n, uint32_t k);
+hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b, float *c, const float *residual,
+                             float *sum, uint32_t m, uint32_t n, uint32_t k);
 // Two independent products of one shape (c0 = a0 b0, c1 = a1 b1) in one
 // launch, for shapes whose plan needs no workspace and no 256x256 tile
 // (gemm_f32_pairable); each output is bit-identical to its own gemm_f32.

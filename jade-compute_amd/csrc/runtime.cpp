@@ -110,10 +110,28 @@ bool fusable_gate_up_swiglu(const jr_dispatch &x, const jr_dispatch &y, const jr
            jade::hipk::gemm_f32_dual_swiglu_fits(g.m, g.n, g.k);
 }
 
+// A GEMM and the Add that follows it run as one launch when the GEMM's output
+// P is one operand of the Add (add(P, X -> O) or add(X, P -> O) over m*n
+// elements), X is not P, and O is neither of the GEMM's inputs (the epilogue
+// writes O while other workgroups still read them): the residual MLP's down
+// projection and residual add (src/runtime/workloads.rs:440-465). P and O are
+// bit-identical to the ordered launches (gemm_f32_residual).
+bool fusable_gemm_residual(const jr_dispatch &x, const jr_dispatch &y) {
+    const KernelSpec &g = spec_of(x), &a = spec_of(y);
+    if (!is_gemm(g) || a.op != Op::Add || x.buffer_count != 3 || y.buffer_count != 3) return false;
+    if (uint64_t(a.len) != uint64_t(g.m) * g.n) return false;
+    void *const p = x.buffers[2];
+    if (y.buffers[0] != p && y.buffers[1] != p) return false;
+    void *const residual = y.buffers[0] == p ? y.buffers[1] : y.buffers[0];
+    void *const o = y.buffers[2];
+    if (residual == p || o == x.buffers[0] || o == x.buffers[1]) return false;
+    return aligned16(x.buffers[0]) && aligned16(x.buffers[1]) && jade::hipk::gemm_f32_residual_fits(g.m, g.n, g.k);
+}
+
 // One launch of the batch: job `first` alone, or it and the one or two jobs
 // after it as one paired or fused launch.
 struct Step {
-    enum class Form { Single, Pair, GateUpSwiglu } form;
+    enum class Form { Single, Pair, GateUpSwiglu, GemmResidual } form;
     size_t first;
 };
 
@@ -125,6 +143,9 @@ std::vector<Step> plan_steps(const jr_dispatch *jobs, size_t n) {
             j += 3;
         } else if (j + 1 < n && pairable(jobs[j], jobs[j + 1])) {
             steps.push_back({Step::Form::Pair, j});
+            j += 2;
+        } else if (j + 1 < n && fusable_gemm_residual(jobs[j], jobs[j + 1])) {
+            steps.push_back({Step::Form::GemmResidual, j});
             j += 2;
         } else {
             steps.push_back({Step::Form::Single, j});
@@ -153,6 +174,13 @@ hipError_t run_step(const Step &step, const jr_dispatch *jobs, hipStream_t q) {
             return jade::hipk::gemm_f32_dual_swiglu(q, cf(x.buffers[0]), cf(x.buffers[1]), cf(y.buffers[1]),
                                                     f(x.buffers[2]), f(y.buffers[2]), f(z.buffers[2]), s.m, s.n,
                                                     s.k);
+        }
+        case Step::Form::GemmResidual: {
+            const KernelSpec &s = spec_of(x);
+            const jr_dispatch &y = jobs[step.first + 1];
+            void *const residual = y.buffers[0] == x.buffers[2] ? y.buffers[1] : y.buffers[0];
+            return jade::hipk::gemm_f32_residual(q, cf(x.buffers[0]), cf(x.buffers[1]), f(x.buffers[2]),
+                                                 cf(residual), f(y.buffers[2]), s.m, s.n, s.k);
         }
     }
     return hipErrorInvalidValue;

@@ -117,3 +117,68 @@ def test_swiglu_writing_a_gemm_input_is_not_fused(runtime):
     ordered = _run_jobs(runtime, specs, arrays, plan, repeats=2, one_at_a_time=True)
     for name in ("g", "u", "wg"):
         np.testing.assert_array_equal(batched[name], ordered[name], err_msg=name)
+
+
+@pytest.mark.parametrize("m,n,k,order", [
+    (4096, 1024, 2816, "px"),  # the C4 down projection: 128x64 LDS-direct tiles
+    (4096, 1024, 2816, "xp"),  # add(X, P -> O): the other operand order
+    (1000, 777, 513, "px"),  # unaligned rows: register-staged tiles with two K groups, edge masks
+    (1024, 1024, 1024, "px"),  # 64x64 tiles with four K groups
+    (4096, 4096, 256, "px"),  # 128x128 tiles
+])
+def test_fused_gemm_residual_is_bit_identical(runtime, m, n, k, order):
+    # gemm(a, w -> p) then add(p, x -> o) run as one launch (the residual
+    # MLP's down projection and residual add); p and o must equal the two
+    # jobs launched one at a time, bit for bit.
+    specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "add": {"op": "add", "len": m * n}}
+    arrays = {"a": orc.normal(m * k, 0x41, 0.0, 0.5), "w": orc.normal(k * n, 0x42, 0.0, 0.05),
+              "x": orc.normal(m * n, 0x43), "p": m * n, "o": m * n}
+    operands = ["p", "x"] if order == "px" else ["x", "p"]
+    plan = [("gemm", ["a", "w", "p"]), ("add", operands + ["o"])]
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
+    for name in ("p", "o"):
+        np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
+    want = orc.gemm_reference(m, n, k, arrays["a"], arrays["w"], rows=(m - 32, m))
+    assert orc.compare(fused["p"][(m - 32) * n:], want, 1e-4, 1e-4).status == 0
+    np.testing.assert_array_equal(fused["o"], fused["p"] + arrays["x"])
+
+
+def test_add_writing_a_gemm_input_is_not_fused(runtime):
+    # add(p, x -> a) overwrites the GEMM's own A (n == k so the lengths
+    # match): fused, the epilogue would write A while other workgroups still
+    # read it, so the batch keeps its order; two repeats make the second
+    # product read the overwritten A.
+    m, n, k = 2048, 1024, 1024
+    specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "add": {"op": "add", "len": m * n}}
+    arrays = {"a": orc.normal(m * k, 0x51, 0.0, 0.05), "w": orc.normal(k * n, 0x52, 0.0, 0.05),
+              "x": orc.normal(m * n, 0x53, 0.0, 0.05), "p": m * n}
+    plan = [("gemm", ["a", "w", "p"]), ("add", ["p", "x", "a"])]
+    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    ordered = _run_jobs(runtime, specs, arrays, plan, repeats=2, one_at_a_time=True)
+    for name in ("a", "p"):
+        np.testing.assert_array_equal(batched[name], ordered[name], err_msg=name)
+
+
+def test_c4_block_fused_equals_ordered_launches(runtime):
+    # The whole C4 block batched (gate/up/SwiGLU and down/Add each fused) is
+    # bit-identical, in every one of its six outputs, to the six jobs launched
+    # one at a time.
+    batch, width, hidden = 4096, 1024, 2816
+    specs = {"norm": {"op": "rms_norm", "rows": batch, "cols": width, "epsilon": 1e-6},
+             "up": {"op": "gemm", "m": batch, "n": hidden, "k": width, "tiled": True},
+             "swiglu": {"op": "swi_glu", "len": batch * hidden},
+             "down": {"op": "gemm", "m": batch, "n": width, "k": hidden, "tiled": True},
+             "add": {"op": "add", "len": batch * width}}
+    arrays = {"x": orc.normal(batch * width, 0x1234), "gamma": orc.values(width, 0x7777, 0.5) + np.float32(1.0),
+              "wg": orc.normal(width * hidden, 0x3333, 0.0, 0.02), "wu": orc.normal(width * hidden, 0x4444, 0.0, 0.02),
+              "wd": orc.normal(hidden * width, 0x5555, 0.0, 0.02), "normalized": batch * width,
+              "gate": batch * hidden, "upv": batch * hidden, "act": batch * hidden, "proj": batch * width,
+              "out": batch * width}
+    plan = [("norm", ["x", "gamma", "normalized"]), ("up", ["normalized", "wg", "gate"]),
+            ("up", ["normalized", "wu", "upv"]), ("swiglu", ["gate", "upv", "act"]), ("down", ["act", "wd", "proj"]),
+            ("add", ["proj", "x", "out"])]
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
+    for name in ("normalized", "gate", "upv", "act", "proj", "out"):
+        np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
