@@ -127,6 +127,20 @@ int jr_fill_values(float *out, size_t len, uint32_t seed, float scale);
  * u2=(s>>8)/2^24, mean + sigma*sqrt(-2 ln u1)*cos(2 pi u2) in FP64. */
 int jr_fill_normal(float *out, size_t len, uint32_t seed, float mean, float sigma);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): C = A B for device pointers A [m,k], B [k,n], C [m,n]
+ * (16-byte aligned A and B), the same kernels and results as a compiled
+ * {"op":"gemm"} pipeline run by jr_execute_dispatches, launched
+ * asynchronously on `stream` (a hipStream_t of the current device; NULL is
+ * the null stream). Nothing is allocated: the split-K partials of small grids
+ * use a static 8 MiB device array that each GPU holds until the process
+ * ends, enough for every plan of the current planner; a shape needing more
+ * is rejected with code 1. Calls that overlap on one GPU race on that array.
+ * Codes as above (1 invalid, 2 runtime). */
+int jr_gemm_f32_noalloc(void *stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n, uint32_t k,
+                        char *err, size_t cap);
+
 #ifdef __cplusplus
 }
 #endif

@@ -316,3 +316,19 @@ def test_online_attention_query_blocks_fit_the_grid():
     assert ok["launch"]["grid"][1] <= 65535
     msg = rejected({"op": "attention_online", "heads": 1, "seq": 65535 * 128 + 1, "dim": 1, "causal": False})
     assert "8388480" in msg
+
+
+def test_noalloc_scratch_covers_every_split_plan():
+    # jr_gemm_f32_noalloc keeps split-K partials in an 8 MiB static device
+    # array; every split plan of this shape grid fits it (the planner splits K
+    # only for grids of at most half the CUs' worth of tiles).
+    limit = 8 << 20
+    dims = (1, 16, 32, 64, 96, 127, 128, 192, 256, 384, 500, 512, 640, 768, 1000, 1536, 3000, 4096, 6000, 16384)
+    most = 0
+    for m in dims:
+        for n in dims:
+            for k in (128, 513, 1024, 4096, 65536):
+                if m * k >= 2 ** 31 or k * n >= 2 ** 31:
+                    continue
+                most = max(most, describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["workspace_bytes"])
+    assert 0 < most <= limit, most
