@@ -532,6 +532,280 @@ size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t sl
     return (n + 3) & ~size_t(3);
 }
 
+// ---- Small grids: 16-query waves splitting keys inside the block -----------
+// For grids whose 128-query blocks cannot fill the chip. A block of four waves
+// owns two 16-query blocks of one head, x and X-1-x (X = ceil(seq/16); one
+// block where the two coincide), so every block does the same work under the
+// causal mask: x+1 and X-x 16-key units, X+1 in all (2X without the mask).
+// The block's units (those of x, then those of the partner) are cut into four
+// equal runs, one per wave; a wave whose run crosses from one query block into
+// the other switches queries there. Each wave loads its own K and V rows from
+// global memory (L2) straight into registers in MFMA operand order, one chunk
+// of units ahead, so the K loop has no LDS staging and no barrier. At the end
+// the waves merge their partial (O, max, normaliser) rows through LDS and
+// store O: no second launch and no workspace.
+//
+// Products run on v_mfma_f32_16x16x4_f32 in transposed form; lane l = 16g + i:
+//  - S^T[key, query] over dims: step s takes dim (DP/4)g + s, so lane l
+//    supplies K[key 16u + i][(DP/4)g + s] (A) and Q[query i][(DP/4)g + s]
+//    (B), DP/4 consecutive floats of one row each. The result leaves lane l
+//    holding query i's scores for keys 16u + 4g + r, r = 0..3, which are the
+//    lane's B operands of the P.V product as they stand.
+//  - O^T[dim, query] += V^T[dim, key] P^T[key, query]: step r takes keys
+//    16u + 4g + r for lane group g, and row i of dim block db is dim
+//    NDB i + db (NDB = DP/16), so lane l's A operands over db are the NDB
+//    consecutive floats V[16u + 4g + r][NDB i ...]: vector loads.
+//  - The O^T accumulators leave lane l holding query i's dims
+//    (DP/4)g + NDB r' + db: DP/4 consecutive floats.
+// Scores are in log2 units (Q pre-scaled by scale * log2(e)), as in the
+// flash kernel above.
+namespace pairs {
+constexpr int kWaves = 4, kThreads = 64 * kWaves;
+constexpr int kUnit = 16;  // keys per unit, queries per query block
+
+template <int DP>
+struct UnitKV {
+    static constexpr int kK = DP / 16, kV = DP / 64;
+    f32x4 k[kK];     // K[16u + i][(DP/4)g + 4t ...], t < DP/16
+    f32x4 v[4][kV];  // V[16u + 4g + r][NDB i + 4e ...], e < NDB/4
+};
+
+// Max and sum over the four lanes of one query (l, l^16, l^32, l^48), in the
+// VALU: v_permlane16_swap pairs rows of 16 lanes, then v_permlane32_swap
+// (above) pairs the two halves of the wave.
+__device__ inline float rows_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float rows_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ inline float lanes_max(float x) { return halves_max(rows_max(x)); }
+__device__ inline float lanes_sum(float x) { return halves_sum(rows_sum(x)); }
+
+// Unconditional loads with row and column indices clamped into the tensors,
+// so the compiler waits for exactly the chunk it consumes. A clamped key row
+// only reaches masked scores (and P = 0 for V); a clamped dim of K meets a
+// zero in Q, and a clamped dim of V only reaches outputs that are not stored.
+template <int DP>
+__device__ inline void load_unit(const float *__restrict__ K, const float *__restrict__ V, size_t base, int key0,
+                                 int seq, int dim, int i, int g, UnitKV<DP> &kv) {
+    constexpr int NDB = DP / 16;
+    const size_t krow = size_t(min(key0 + i, seq - 1)) * dim;
+#pragma unroll
+    for (int t = 0; t < UnitKV<DP>::kK; ++t) {
+        const int d = min((DP / 4) * g + 4 * t, dim - 4);
+        kv.k[t] = *reinterpret_cast<const f32x4 *>(K + base + krow + d);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const size_t vrow = size_t(min(key0 + 4 * g + r, seq - 1)) * dim;
+#pragma unroll
+        for (int e = 0; e < UnitKV<DP>::kV; ++e) {
+            const int d = min(NDB * i + 4 * e, dim - 4);
+            kv.v[r][e] = *reinterpret_cast<const f32x4 *>(V + base + vrow + d);
+        }
+    }
+}
+}  // namespace pairs
+
+// Grid: heads * ceil(X / 2) blocks, block b = pair b / heads of head b % heads.
+// Needs dim % 4 == 0 and 16-byte aligned tensors (vector loads), dim <= DP.
+template <int DP, bool CAUSAL, int CH>
+__global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const float *__restrict__ Q,
+                                                                        const float *__restrict__ K,
+                                                                        const float *__restrict__ V,
+                                                                        float *__restrict__ O, int seq, int dim,
+                                                                        float qscale, int heads) {
+    using namespace pairs;
+    using KV = UnitKV<DP>;
+    constexpr int D4 = DP / 4, NDB = DP / 16;
+    __shared__ f32x4 part[kWaves * 2][kUnit][D4];  // DP floats per query row
+    __shared__ float2 mls[kWaves * 2][kUnit];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // uniform: scalar loop control
+    const int i = lane & 15, g = lane >> 4;
+    const int blocks_q = (seq + kUnit - 1) / kUnit;  // query blocks, and key units
+    const int head = int(blockIdx.x) % heads, pair = int(blockIdx.x) / heads;
+    const int xa = pair, xb = blocks_q - 1 - pair;  // xa <= xb
+    const bool single = xa == xb;
+    // Key units [0, uc) serve both query blocks, [uc, ub) only xb (xa's keys
+    // are a prefix of xb's under the causal mask, and all of them without it).
+    const int ub = CAUSAL ? xb + 1 : blocks_q;
+    const int uc = single ? 0 : (CAUSAL ? xa + 1 : blocks_q);
+    // A shared unit costs two units of work, an xb-only unit one. Wave w
+    // takes the units between the w-th and (w+1)-th quarter of the cost.
+    const int cost = 2 * uc + (ub - uc);
+    auto unit_at = [&](int c) { return c <= 2 * uc ? (c + 1) / 2 : c - uc; };
+    const int u0 = unit_at(cost * wave / kWaves), u1 = unit_at(cost * (wave + 1) / kWaves);
+    const size_t base = size_t(head) * size_t(seq) * size_t(dim);
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+
+    // A chunk is up to CH units that are all shared or all xb-only.
+    auto chunk_end = [&](int t) { return min(u1, min(t + CH, t < uc ? uc : ub)); };
+    // Every chunk loads CH units; positions past the chunk's end re-read its
+    // last unit and are never used.
+    auto load_chunk = [&](KV(&buf)[CH], int t) {
+        const int e = chunk_end(t);
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            pairs::load_unit<DP>(K, V, base, min(t + c, e - 1) * kUnit, seq, dim, i, g, buf[c]);
+    };
+
+    // Both query blocks' Q rows, scaled; dims past `dim` are zero.
+    float qa[D4], qb[D4];
+    auto load_q = [&](int x, float(&dst)[D4]) {
+        const size_t row = size_t(min(x * kUnit + i, seq - 1)) * dim;
+#pragma unroll
+        for (int s4 = 0; s4 < D4 / 4; ++s4) {
+            const int d = D4 * g + 4 * s4;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(Q + base + row + min(d, dim - 4));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[4 * s4 + e] = d < dim ? v[e] * qscale : 0.f;
+        }
+    };
+    load_q(xa, qa);
+    load_q(xb, qb);
+
+    struct State {
+        f32x4 acc[NDB];
+        float row_max, row_sum;
+    };
+    State sa, sb;
+#pragma unroll
+    for (int b = 0; b < NDB; ++b) sa.acc[b] = sb.acc[b] = zero4;
+    sa.row_max = sb.row_max = -INFINITY;
+    sa.row_sum = sb.row_sum = 0.f;
+
+    // One chunk of n units starting at unit t for the 16 queries of block x.
+    auto attend = [&](const KV(&kv)[CH], int t, int n, int x, const float(&q)[D4], State &st) {
+        const int query = x * kUnit + i;
+        f32x4 s[CH];
+        float tile_max = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            s[c] = zero4;
+            if (c < n) {
+#pragma unroll
+                for (int d = 0; d < D4; ++d)
+                    s[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], q[d], s[c], 0, 0, 0);
+                const int key0 = (t + c) * kUnit;
+                // Only a unit on the causal diagonal or past the end of seq
+                // holds masked keys (wave-uniform).
+                if ((CAUSAL && t + c == x) || key0 + kUnit > seq) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int key = key0 + 4 * g + r;
+                        if (!(key < seq && (!CAUSAL || key <= query))) s[c][r] = -INFINITY;
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tile_max = fmaxf(tile_max, s[c][r]);
+            }
+        }
+        // Every query of a processed chunk has a live key (the first key of
+        // each unit lies at or below the diagonal and inside seq), so the
+        // running max is finite from the first chunk on.
+        tile_max = pairs::lanes_max(tile_max);
+        const float next_max = fmaxf(st.row_max, tile_max);
+        const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
+        float tile_sum = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            if (c < n) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - next_max);
+                    tile_sum += s[c][r];
+                }
+            }
+        st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
+        st.row_max = next_max;
+        if (__any(old_weight != 1.0f)) {
+#pragma unroll
+            for (int b = 0; b < NDB; ++b) st.acc[b] *= old_weight;
+        }
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            if (c < n) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int b = 0; b < NDB; ++b)
+                        st.acc[b] =
+                            __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r], st.acc[b], 0, 0, 0);
+            }
+    };
+    auto process = [&](const KV(&kv)[CH], int t) {
+        const int n = chunk_end(t) - t;
+        if (t < uc) attend(kv, t, n, xa, qa, sa);
+        attend(kv, t, n, xb, qb, sb);
+    };
+
+    // Two chunk buffers: the next chunk's loads are in flight while the
+    // current one is consumed (the last prefetch re-reads the last chunk).
+    KV buf0[CH], buf1[CH];
+    if (u0 < u1) {
+        int t = u0;
+        load_chunk(buf0, t);
+        for (;;) {
+            int e = chunk_end(t);
+            load_chunk(buf1, e < u1 ? e : t);
+            process(buf0, t);
+            t = e;
+            if (t >= u1) break;
+            e = chunk_end(t);
+            load_chunk(buf0, e < u1 ? e : t);
+            process(buf1, t);
+            t = e;
+            if (t >= u1) break;
+        }
+    }
+
+    // Partial rows to LDS: slot (wave, 0) for xa, (wave, 1) for xb. A block
+    // this wave did not touch leaves (max -inf, sum 0, zero row): weight 0 in
+    // the merge.
+    auto flush = [&](const State &st, int slot) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int e = 0; e < NDB / 4; ++e) {
+                const f32x4 o = {st.acc[4 * e][r], st.acc[4 * e + 1][r], st.acc[4 * e + 2][r], st.acc[4 * e + 3][r]};
+                part[slot][i][(D4 * g + NDB * r) / 4 + e] = o;
+            }
+        if (g == 0) mls[slot][i] = make_float2(st.row_max, st.row_sum);
+    };
+    flush(sa, wave * 2);
+    flush(sb, wave * 2 + 1);
+    __syncthreads();
+
+    // Merge: thread -> (query block, query, 4 dims). With a single query
+    // block, slot 1 of every wave holds it.
+    for (int o = int(threadIdx.x); o < 2 * kUnit * D4; o += kThreads) {
+        const int seg = o / (kUnit * D4), rest = o % (kUnit * D4);
+        const int qi = rest / D4, d4 = rest % D4;
+        if (seg == 0 && single) continue;
+        const int q = (seg ? xb : xa) * kUnit + qi, d = 4 * d4;
+        if (q >= seq || d >= dim) continue;
+        float top = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) top = fmaxf(top, mls[w * 2 + seg][qi].x);
+        f32x4 num = zero4;
+        float den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float2 ml = mls[w * 2 + seg][qi];
+            const float wt = __builtin_amdgcn_exp2f(ml.x - top);
+            den = fmaf(wt, ml.y, den);
+            num += wt * part[w * 2 + seg][qi][d4];
+        }
+        const float inv = 1.0f / den;
+        *reinterpret_cast<f32x4 *>(O + base + size_t(q) * dim + d) = num * inv;
+    }
+}
+
 template <int DP, int NW, bool CAUSAL, bool SPLIT>
 hipError_t launch_online(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                          float2 *ml, uint32_t heads, uint32_t seq, uint32_t dim, SplitPlan plan, bool vec) {
@@ -548,9 +822,41 @@ hipError_t launch_online(hipStream_t stream, const float *q, const float *k, con
     return hipGetLastError();
 }
 
+
+// Blocks of the paired 16-query launch: heads x ceil(X / 2), X = ceil(seq / 16).
+uint32_t pair_blocks(uint32_t heads, uint32_t seq) { return heads * (((seq + 15) / 16 + 1) / 2); }
+
+// Grids that would split keys across blocks run the paired 16-query kernel
+// instead when its rows take vector loads (dim % 4 == 0), the head dim pads
+// to 64 or 128, and it has at least kPairsMinBlocks blocks; smaller grids
+// keep the split launch, which spreads any grid over every CU.
+constexpr uint32_t kPairsMinBlocks = 128;
+bool use_pairs(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    return split_plan(heads, seq, causal).slices > 1 && dim % 4 == 0 && padded_dim(dim) >= 64 &&
+           pair_blocks(heads, seq) >= kPairsMinBlocks;
+}
+
+template <int DP, int CH>
+hipError_t launch_pairs(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
+                        uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
+    const dim3 grid(pair_blocks(heads, seq)), block(pairs::kThreads);
+    if (causal)
+        hipLaunchKernelGGL((attention_pairs_mfma<DP, true, CH>), grid, block, 0, stream, q, k, v, out, int(seq),
+                           int(dim), qscale, int(heads));
+    else
+        hipLaunchKernelGGL((attention_pairs_mfma<DP, false, CH>), grid, block, 0, stream, q, k, v, out, int(seq),
+                           int(dim), qscale, int(heads));
+    return hipGetLastError();
+}
+
 template <int DP>
 hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                         float *workspace, uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
+    if constexpr (DP >= 64) {
+        if (vec && use_pairs(heads, seq, dim, causal))
+            return launch_pairs<DP, DP == 64 ? 2 : 1>(stream, q, k, v, out, heads, seq, dim, causal);
+    }
     const SplitPlan plan = split_plan(heads, seq, causal);
     if (plan.slices > 1) {
         // Split grids are small grids, which always take four-wave blocks.
@@ -585,6 +891,11 @@ uint32_t lds_bytes(int nw) {
 
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
     const int dp = padded_dim(dim);
+    if (use_pairs(heads, seq, dim, causal))
+        return {dp == 64 ? "attention_online_mfma16_d64_pairs" : "attention_online_mfma16_d128_pairs",
+                {pair_blocks(heads, seq), 1, 1},
+                {uint32_t(pairs::kThreads), 1, 1},
+                uint32_t(pairs::kWaves * 2 * pairs::kUnit * (dp * sizeof(float) + sizeof(float2)))};
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
     const SplitPlan plan = split_plan(heads, seq, causal);
@@ -600,6 +911,7 @@ LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, b
 }
 
 size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    if (use_pairs(heads, seq, dim, causal)) return 0;
     const uint32_t splits = split_plan(heads, seq, causal).slices;
     if (splits <= 1) return 0;
     return (split_part_floats(heads, seq, dim, splits) + 2 * size_t(splits) * heads * seq) * sizeof(float);

@@ -138,8 +138,8 @@ def test_scale_is_one_over_sqrt_dim(runtime):
     assert got[0, 0] == pytest.approx(0.5, rel=2e-6)
 
 
-@pytest.mark.parametrize("h,s,d,causal", [(8, 1024, 64, True), (1, 700, 128, True), (2, 513, 32, False),
-                                          (1, 4096, 64, True), (3, 200, 5, True)])
+@pytest.mark.parametrize("h,s,d,causal", [(2, 1024, 64, True), (1, 700, 128, True), (2, 513, 32, False),
+                                          (1, 2048, 64, True), (3, 200, 5, True)])
 def test_split_key_grids(runtime, h, s, d, causal):
     # Grids smaller than the chip split the keys into slices (one block per
     # live slice) and merge them; a causal slice can hold no live key for some
@@ -149,6 +149,27 @@ def test_split_key_grids(runtime, h, s, d, causal):
     assert launch["kernel"].endswith("_split") and launch["grid"][0] > h and launch["grid"][1] == 1, launch
     n = h * s * d
     q, k, v = orc.normal(n, 0x4444), orc.normal(n, 0x5555), orc.normal(n, 0x6666)
+    got = run_online(runtime, h, s, d, causal, q, k, v, repeats=2)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("h,s,d,causal", [
+    (8, 1024, 64, True), (8, 1024, 64, False),  # config C3: 256 blocks of two 16-query blocks
+    (8, 1000, 64, True),  # odd count of 16-query blocks (the middle one alone), ragged last block and unit
+    (12, 700, 48, False),  # head dim padded to 64
+    (16, 512, 128, True), (32, 256, 100, True),  # head dims 128 and 100 (padded to 128)
+    (1, 4096, 64, True),  # one head, 128 blocks
+])
+def test_paired_small_grids(runtime, h, s, d, causal):
+    # Grids that would otherwise split keys across blocks run 16-query waves
+    # that split each block's keys among themselves and merge in LDS: one
+    # launch, no workspace.
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
+    assert kernel.launch["kernel"].endswith("_pairs") and kernel.description["workspace_bytes"] == 0, kernel.launch
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x4141), orc.normal(n, 0x4242), orc.normal(n, 0x4343)
     got = run_online(runtime, h, s, d, causal, q, k, v, repeats=2)
     want = orc.attention_reference(h, s, d, causal, q, k, v)
     check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)

@@ -215,7 +215,11 @@ def test_descriptions_report_workspace_bytes():
     assert describe({"op": "gemm", "m": 256, "n": 256, "k": 4096, "tiled": True})["workspace_bytes"] == 16 * 256 * 256 * 4
     assert describe({"op": "gemm", "m": 512, "n": 512, "k": 512, "tiled": True})["workspace_bytes"] == 0
     assert describe({"op": "gemm", "m": 4096, "n": 4096, "k": 4096, "tiled": True})["workspace_bytes"] == 0
-    assert describe({"op": "attention_online", "heads": 8, "seq": 1024, "dim": 64, "causal": True})["workspace_bytes"] > 0
+    assert describe({"op": "attention_online", "heads": 2, "seq": 1024, "dim": 64, "causal": True})["workspace_bytes"] > 0
+    # Config C3 runs the paired 16-query kernel: one launch, no workspace.
+    c3 = describe({"op": "attention_online", "heads": 8, "seq": 1024, "dim": 64, "causal": True})
+    assert c3["workspace_bytes"] == 0 and c3["launch"]["kernel"] == "attention_online_mfma16_d64_pairs"
+    assert c3["launch"]["grid"] == [256, 1, 1]
     assert describe({"op": "attention_online", "heads": 128, "seq": 4096, "dim": 128, "causal": True})[
         "workspace_bytes"] == 0
     assert describe({"op": "softmax", "rows": 4, "cols": 4})["workspace_bytes"] == 0
