@@ -341,6 +341,25 @@ def bench_copy(rt, steps, warmup):
     return out
 
 
+def bench_floor(rt, steps, warmup):
+    """Per-launch time of near-empty launches back to back on the runtime's
+    stream: the dispatch floor under every short kernel (one workgroup copying
+    64 floats; 256 workgroups adding 262144 floats, 1 MiB per operand)."""
+    out = {}
+    for name, spec, n in (("copy_64", {"op": "elementwise", "len": 64, "inputs": 1,
+                                        "expression": {"kind": "input", "binding": 0}}, 64),
+                          ("add_256_workgroups", {"op": "add", "len": 262144}, 262144)):
+        kernel = rt.compile(spec)
+        count = spec.get("inputs", 2)
+        bufs = [rt.resident(jade_hip.fill_values(n, 0x77 + i, 1.0)) for i in range(count)] + [rt.alloc(n)]
+        t = measure({name: Workload(rt, [(kernel, bufs)])}, steps, warmup)[name]
+        out[name] = {"us_per_launch": 1e3 * t["ms_per_step"], "min_us": 1e3 * t["min_ms_per_step"],
+                     "launch": kernel.launch}
+        for b in bufs:
+            b.free()
+    return out
+
+
 def _read_csv(path):
     import csv
 
@@ -421,8 +440,11 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
 # SQ_VALU_MFMA_BUSY_CYCLES below the 2^31 at which the counter saturates, and
 # each exercises one production kernel (128x128 and 128x64 GEMM tiles, 64x64
 # tiles with four K groups, direct-load 32x32 tiles, the 256x256 tile with a
-# 64x64 tail; the split-key, four-wave and eight-wave attention launches).
-MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024), (512, 512, 512), (5120, 5120, 1024))
+# 64x64 tail, unaligned rows on 64x64 tiles with two K groups, the MLP's down
+# projection with its residual epilogue shape, direct-load tiles split over K;
+# the split-key, four-wave and eight-wave attention launches).
+MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024), (512, 512, 512), (5120, 5120, 1024),
+              (1000, 777, 513), (4096, 1024, 2816), (16, 1024, 2816))
 MFMA_ATTENTION = ((8, 1024, 64, False), (8, 1024, 64, True), (32, 2048, 64, True), (64, 2048, 128, True))
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 XCDS = 8
@@ -540,7 +562,7 @@ def main():
     ap.add_argument("--preheat-ms", type=float, default=PREHEAT_MS,
                     help="untimed device time of each workload before its samples (0 for counter runs)")
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma"])
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma", "floor"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--summarize-rocprof", metavar="TRACE_DIR",
                     help="print per-kernel tables from a rocprofv3 --kernel-trace output directory and exit")
@@ -614,6 +636,8 @@ def main():
         extra["rows_mlp_shapes"] = bench_rows(rt, 4096, 1024, 2816, K, W)
     if wl in ("all", "copy"):
         extra["copy_calibration"] = bench_copy(rt, K, W)
+    if wl == "floor":  # launch-floor measurement only; not part of the default line
+        extra["launch_floor"] = bench_floor(rt, max(K, 200), W)
     if wl == "mfma":  # counter runs only; not part of the default line
         extra["mfma_shapes"] = bench_mfma_shapes(rt, K, W)
     if wl in ("all", "sweep"):
