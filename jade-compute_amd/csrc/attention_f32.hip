@@ -738,8 +738,73 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
                             __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r], st.acc[b], 0, 0, 0);
             }
     };
+    // A whole shared chunk: both query blocks in one branch-free basic block,
+    // so the scheduler can overlap one block's softmax with the other's MFMAs.
+    // Masks are selects on a wave-uniform flag; the rescale is unconditional.
+    auto both_full = [&](const KV(&kv)[CH], int t) {
+        f32x4 s_a[CH], s_b[CH];
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            s_a[c] = zero4;
+            s_b[c] = zero4;
+#pragma unroll
+            for (int d = 0; d < D4; ++d) {
+                s_a[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qa[d], s_a[c], 0, 0, 0);
+                s_b[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qb[d], s_b[c], 0, 0, 0);
+            }
+        }
+        auto update = [&](f32x4(&s)[CH], int x, State &st) {
+            const int query = x * kUnit + i;
+            float tile_max = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+                const int key0 = (t + c) * kUnit;
+                const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int key = key0 + 4 * g + r;
+                    const bool live = key < seq && (!CAUSAL || key <= query);
+                    s[c][r] = (masked_unit && !live) ? -INFINITY : s[c][r];
+                    tile_max = fmaxf(tile_max, s[c][r]);
+                }
+            }
+            tile_max = pairs::lanes_max(tile_max);
+            const float next_max = fmaxf(st.row_max, tile_max);
+            const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
+            float tile_sum = 0.f;
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - next_max);
+                    tile_sum += s[c][r];
+                }
+            st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
+            st.row_max = next_max;
+#pragma unroll
+            for (int b = 0; b < NDB; ++b) st.acc[b] *= old_weight;
+        };
+        auto pv = [&](const f32x4(&s)[CH], State &st) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int b = 0; b < NDB; ++b)
+                        st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r],
+                                                                         st.acc[b], 0, 0, 0);
+        };
+        update(s_a, xa, sa);
+        update(s_b, xb, sb);
+        pv(s_a, sa);
+        pv(s_b, sb);
+    };
     auto process = [&](const KV(&kv)[CH], int t) {
         const int n = chunk_end(t) - t;
+        if (t < uc && n == CH) {
+            both_full(kv, t);
+            return;
+        }
         if (t < uc) attend(kv, t, n, xa, qa, sa);
         attend(kv, t, n, xb, qb, sb);
     };
