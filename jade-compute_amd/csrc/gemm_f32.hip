@@ -1020,13 +1020,28 @@ struct Slice {
     float b[16];  // B[k0 + 16h + s][col c] at b[s]
 };
 
-// A 4-float run clamped to start at most at K - 4 stays inside its row.
-__device__ inline void load_slice(const float *__restrict__ A, const float *__restrict__ B, int K, int N,
-                                  size_t arow, int lda, int bcol, int k0, int h, Slice &s) {
+// Aligned rows (K % 4 == 0): a 4-float run clamped to start at most at
+// K - 4 stays inside its row. Unaligned rows (BUFA): buffer loads at
+// 4-byte-aligned offsets, unclamped: a run that crosses the end of its row
+// reads the next row's first floats at k >= K (zeroed when consumed), and
+// the buffer's range check returns zero past the end of A.
+template <bool BUFA>
+__device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_rsrc_t ra,
+                                  const float *__restrict__ B, int K, int N, size_t arow, int lda, int bcol, int k0,
+                                  int h, Slice &s) {
     const int kb = k0 + 16 * h;
-    const float *ap = A + arow * lda;
+    if constexpr (BUFA) {
+        const uint32_t first = (uint32_t(arow) * uint32_t(lda) + uint32_t(kb)) * 4u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) s.a[q] = *reinterpret_cast<const f32x4 *>(ap + min(kb + 4 * q, K - 4));
+        for (int q = 0; q < 4; ++q) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, int(first + 16u * q), 0, 0);
+            s.a[q] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+        }
+    } else {
+        const float *ap = A + arow * lda;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s.a[q] = *reinterpret_cast<const f32x4 *>(ap + min(kb + 4 * q, K - 4));
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) s.b[e] = B[size_t(min(kb + e, K - 1)) * N + bcol];
 }
@@ -1051,13 +1066,17 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 // gridDim.y > 1: a batch of independent products, product z at A + z*sa,
 // B + z*sb, C + z*sc (attention's P.V per head, or the K slices of a split
 // product: sa = K, sb = K*N with A rows lda apart).
-template <int G>
+// BUFA: A rows are not 16-byte aligned (K % 4 != 0); A is read through buffer
+// loads, which needs M*K*4 < 2^31 and no batch (lda = K).
+template <int G, bool BUFA = false>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
                                                           float *__restrict__ C, int M, int N, int K, int lda,
                                                           int tiles_m, int tiles_n, size_t sa = 0, size_t sb = 0,
                                                           size_t sc = 0) {
     using namespace direct;
     constexpr int D = kDepth;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(A), 0, BUFA ? int(uint32_t(M) * uint32_t(K) * 4u) : 0, int(kBufferWord3));
     __shared__ float red[(G > 1 ? G - 1 : 1) * 16 * 64];
     A += blockIdx.y * sa;
     B += blockIdx.y * sb;
@@ -1083,7 +1102,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
     if (count > 0) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            load_slice(A, B, K, N, arow, lda, bcol, slice_k(d), h, buf[d]);
+            load_slice<BUFA>(A, ra, B, K, N, arow, lda, bcol, slice_k(d), h, buf[d]);
             __builtin_amdgcn_sched_barrier(0);  // loads issued slice by slice
         }
         int i = 0;
@@ -1091,7 +1110,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 mma_slice(buf[d], valid(i + d), acc);
-                load_slice(A, B, K, N, arow, lda, bcol, slice_k(i + d + D), h, buf[d]);
+                load_slice<BUFA>(A, ra, B, K, N, arow, lda, bcol, slice_k(i + d + D), h, buf[d]);
                 // Keep the slices in order: interleaving their independent
                 // MFMA chains would make the first one wait for every load.
                 __builtin_amdgcn_sched_barrier(0);
@@ -1148,6 +1167,7 @@ struct Plan {
     int direct;     // > 0: gemm_f32_direct with this many waves (tiles_m/tiles_n count 32x32 tiles)
     int kgroups;    // 2 or 4: 64x64 tiles with that many K groups of four waves (0 or 1: one group)
     int tail_tm, tail_tn;  // big plans: the partial last round's tile, (64*tail_tm) x (64*tail_tn)
+    bool bufa;             // direct plans over unaligned A rows: A through buffer loads
 };
 
 constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
@@ -1295,6 +1315,26 @@ int edge_free_choice(uint32_t m, uint32_t n, uint32_t k, int old) {
     return cost(old) > 1.05 * cost(cand) ? cand : old;
 }
 
+// Unaligned rows (K % 4 != 0) on grids of at most half the CUs' worth of
+// 64x64 tiles run the direct-load 32x32 tiles too, with A through buffer
+// loads, when K has at most 24 slices of 32 and the grid at least 64 tiles of
+// 32x32 (the split-K 64x64 plans otherwise). Measured on MI355X against them:
+// 500x777x513 17.9 -> 12.4 us, 100x777x513 10.2 -> 8.3. On larger grids the
+// direct tiles lose to the LDS-staged 64x64 tiles with two K groups
+// (1000x777x513: 15.6 us against 20.8 with 32x32 tiles and 20.1 with 32x64
+// tiles whose waves share each A operand between two MFMA chains).
+int direct_waves_unaligned(uint32_t m, uint32_t n, uint32_t k) {
+    if (k % 4 == 0 || !unaligned_buffers_fit(m, n, k)) return 0;
+    const uint64_t t64 = uint64_t((m + 63) / 64) * ((n + 63) / 64);
+    const uint64_t t32 = uint64_t((m + 31) / 32) * ((n + 31) / 32);
+    if (t64 > uint64_t(kCUs / 2) || t32 < 64) return 0;
+    const uint32_t slices = (k + kBK - 1) / kBK;
+    if (slices > 4 * 6) return 0;
+    int g = 4;
+    while (g > 1 && uint32_t(g) > slices) g /= 2;
+    return g;
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
@@ -1327,9 +1367,12 @@ Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
         const int pick = edge_free_choice(m, n, k, best >= 0 ? best : 2);
         return grid(shapes[pick][0], shapes[pick][1]);
     }
-    if (t <= kCUs / 2)
+    if (t <= kCUs / 2) {
         if (const int g = direct_waves(m, n, k))
             return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1, 0, 0};
+        if (const int g = direct_waves_unaligned(m, n, k))
+            return {1, 1, 1, kchunk, int((m + 31) / 32), int((n + 31) / 32), false, 0, g, 1, 0, 0, true};
+    }
     if (const int s = skinny_slices(m, n, k))
         return {1, 1, s, int(k / s), 1, int((n + 31) / 32), false, 0, 4, 1, 0, 0};
     if (t <= kCUs / 2) {
@@ -1404,7 +1447,7 @@ Route route_for(uint32_t m, uint32_t n, uint32_t k) {
         return r;
     }
     if (p.direct) {
-        r.launchable = r.launchable && k % 4 == 0 && (p.slices == 1 || p.direct == 4);
+        r.launchable = r.launchable && (k % 4 == 0 ? (p.slices == 1 || p.direct == 4) : (p.bufa && p.slices == 1));
         return r;
     }
     // A four-group plan whose loads would take the clamped global loads
@@ -1485,7 +1528,10 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     if (p.direct) {
         static const char *names[3] = {"gemm_f32_direct_32x32x32_w1", "gemm_f32_direct_32x32x32_w2",
                                        "gemm_f32_direct_32x32x32_w4"};
-        return {p.slices > 1 ? "gemm_f32_direct_32x32x32_w4_splitk" : names[p.direct == 4 ? 2 : p.direct - 1],
+        static const char *buf_names[3] = {"gemm_f32_direct_32x32x32_w1_buf", "gemm_f32_direct_32x32x32_w2_buf",
+                                           "gemm_f32_direct_32x32x32_w4_buf"};
+        const int w = p.direct == 4 ? 2 : p.direct - 1;
+        return {p.slices > 1 ? "gemm_f32_direct_32x32x32_w4_splitk" : p.bufa ? buf_names[w] : names[w],
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {uint32_t(64 * p.direct), 1, 1},
                 uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
@@ -1606,6 +1652,16 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
             if (status != hipSuccess) return status;
             hipLaunchKernelGGL(splitk_reduce, dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, stream, workspace, c, mn,
                                p.slices);
+        } else if (p.bufa) {
+            if (p.direct == 4)
+                hipLaunchKernelGGL((gemm_f32_direct<4, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
+                                   int(k), p.tiles_m, p.tiles_n);
+            else if (p.direct == 2)
+                hipLaunchKernelGGL((gemm_f32_direct<2, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
+                                   int(k), p.tiles_m, p.tiles_n);
+            else
+                hipLaunchKernelGGL((gemm_f32_direct<1, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
+                                   int(k), p.tiles_m, p.tiles_n);
         } else if (p.direct == 4) {
             hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
                                p.tiles_m, p.tiles_n);

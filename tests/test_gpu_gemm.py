@@ -128,6 +128,22 @@ def test_direct_tile_shapes(runtime, m, n, k, waves):
     gate(got, m, n, k, a, b)
 
 
+@pytest.mark.parametrize("m,n,k,waves", [(500, 777, 513, 4), (100, 777, 513, 4), (333, 555, 101, 4),
+                                          (777, 300, 255, 4), (250, 300, 35, 2), (300, 300, 1, 1), (4100, 3, 9, 1)])
+def test_direct_tiles_over_unaligned_rows(runtime, m, n, k, waves):
+    # Small grids with K % 4 != 0 run the direct-load 32x32 kernel with A read
+    # through buffer loads at 4-byte-aligned offsets: a run crossing the end of
+    # its row reads the next row (zeroed past K), the buffer's range check
+    # zeroes runs past the end of A; ragged M and N as for aligned rows.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == f"gemm_f32_direct_32x32x32_w{waves}_buf", kernel.launch
+    assert kernel.description["workspace_bytes"] == 0
+    a = orc.values(m * k, 0x9B, 1.0)
+    b = orc.values(k * n, 0xAB, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    gate(got, m, n, k, a, b)
+
+
 @pytest.mark.parametrize("m,n,k,kernel", [
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # register-staged (unaligned), last group partial

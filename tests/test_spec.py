@@ -192,6 +192,7 @@ def test_constant_bits_round_trip():
     (3648, 3648, 1024, "gemm_f32_mfma_64x64x32", [3249, 1, 1]),  # 128x128 would leave edge tiles
     (12288, 1024, 1024, "gemm_f32_mfma_128x64x32", [1536, 1, 1]),  # 128x128 predicted < 5% faster: kept
     (4096, 2816, 1024, "gemm_f32_mfma_128x64x32", [1408, 1, 1]),  # MLP gate/up
+    (500, 777, 513, "gemm_f32_direct_32x32x32_w4_buf", [400, 1, 1]),  # unaligned, <= half the CUs: buffer loads
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
     # Grids of >= 256 tiles of 256x256 as 128x128 tiles, unless that grid's
@@ -306,7 +307,8 @@ def test_every_gemm_shape_routes_to_a_launch():
         d = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
         assert d["hip_supported"] and d["launch"]["kernel"], (m, n, k, d["hip_error"])
         seen.add(d["launch"]["kernel"])
-    families = {"gemm_f32_mfma_256x256x32_tail64x64", "gemm_f32_mfma_256x256x32_tail128x128", "gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x64x32",
+    families = {"gemm_f32_mfma_256x256x32_tail64x64", "gemm_f32_mfma_256x256x32_tail128x128",
+                "gemm_f32_direct_32x32x32_w4_buf", "gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x64x32",
                 "gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_k2", "gemm_f32_mfma_64x64x32_k4",
                 "gemm_f32_mfma_64x64x32_splitk_k2", "gemm_f32_direct_32x32x32_w4",
                 "gemm_f32_direct_32x32x32_w4_splitk"}
