@@ -10,12 +10,13 @@ sweep and the copy calibration.
 
 Timing follows the reference's harness (src/runtime/metal_lab.rs:75-107,
 179-187): each workload gets W untimed warm-up steps and a time-based
-pre-heat (--preheat-ms of device time, reported as `preheat_ms`), then its K
-timed steps run as nine samples, interleaved with the other headline workload
-in rotating order, each sample timed by hipEvents around its launches on the
-runtime's stream (the jr_execute scope, native/jade_runtime_corex.cpp:
-148-189). The reported per-step time is the median sample; the mean and the
-extremes are listed beside it. Bandwidth-bound ops are rotated over copies of
+pre-heat (--preheat-ms of device time, reported as `preheat_ms`), then nine
+samples, interleaved with the other headline workload in rotating order, each
+timed by hipEvents around its launches on the runtime's stream (the
+jr_execute scope, native/jade_runtime_corex.cpp:148-189). The headline's
+samples split exactly K timed steps; every other workload's samples hold at
+least the reference's ten repeats each. The reported per-step time is the
+median sample; the mean and the extremes are listed beside it. Bandwidth-bound ops are rotated over copies of
 their buffers that exceed the 256 MB MALL three times, so their GB/s are HBM
 figures.
 
@@ -110,15 +111,25 @@ class Workload:
                 "preheat_ms": self.preheat_ms, "ms_per_launch": median(self.samples) / self.launches}
 
 
-def measure(workloads, steps, warmup):
-    """Warm-up, pre-heat, then `steps` timed steps of each workload as
-    interleaved samples: sample round r runs the workloads in an order rotated
-    by r (metal_lab.rs:179-187). Returns {name: summary}."""
+# Steps per sample outside the headline: the reference's ten repeats per
+# sample (reports/METAL_ADVANCES.md:109-112), or more when `steps` asks.
+SAMPLE_REPEATS = 10
+
+
+def measure(workloads, steps, warmup, min_repeats=SAMPLE_REPEATS):
+    """Warm-up, pre-heat, then SAMPLES interleaved samples of each workload:
+    sample round r runs the workloads in an order rotated by r
+    (metal_lab.rs:179-187). The samples split `steps` evenly, each holding at
+    least `min_repeats` steps (1 for the headline, which times exactly
+    `steps`). Returns {name: summary}."""
     names = list(workloads)
     for name in names:
         workloads[name].warm(warmup)
         workloads[name].preheat()
-    for r, size in enumerate(split_steps(steps)):
+    sizes = [max(size, min_repeats) for size in split_steps(steps)]
+    if len(sizes) < SAMPLES and min_repeats > 1:
+        sizes += [min_repeats] * (SAMPLES - len(sizes))
+    for r, size in enumerate(sizes):
         for off in range(len(names)):
             workloads[names[(r + off) % len(names)]].sample(size)
     return {name: workloads[name].summary() for name in names}
@@ -607,7 +618,7 @@ def main():
         if wl in ("all", "attention"):
             heads["attention"] = prepare_attention(rt, 128, 4096, 128, True, keep)
         log(f"headline {', '.join(heads)} ...")
-        timing = measure({name: p.workload for name, p in heads.items()}, K, W)
+        timing = measure({name: p.workload for name, p in heads.items()}, K, W, min_repeats=1)
         if "gemm" in heads:
             gemm = finish_gemm(rt, heads["gemm"], timing["gemm"])
             log(f"  gemm 4096^3 {gemm['tflops']:.2f} TFLOP/s")
@@ -679,7 +690,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": config,
-        "timing": {"method": f"median of {head['samples']} interleaved samples over the {K} timed steps, after "
+        "timing": {"method": f"median of {head['samples']} interleaved samples over exactly the {K} timed steps, after "
                              f"{W} warm-up steps and a {PREHEAT_MS:.0f} ms time-based pre-heat per workload",
                    "median_ms_per_step": head["ms_per_step"], "mean_ms_per_step": head["mean_ms_per_step"],
                    "min_ms_per_step": head["min_ms_per_step"], "max_ms_per_step": head["max_ms_per_step"],
