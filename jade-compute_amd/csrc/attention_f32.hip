@@ -31,6 +31,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace jade {
 namespace hipk {
@@ -562,6 +563,7 @@ size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t sl
 namespace pairs {
 constexpr int kWaves = 4, kThreads = 64 * kWaves;
 constexpr int kUnit = 16;  // keys per unit, queries per query block
+constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
 
 template <int DP>
 struct UnitKV {
@@ -589,15 +591,19 @@ __device__ inline float lanes_sum(float x) { return halves_sum(rows_sum(x)); }
 // only reaches masked scores (and P = 0 for V); a clamped dim of K meets a
 // zero in Q, and a clamped dim of V only reaches outputs that are not stored.
 template <int DP>
-__device__ inline void load_unit(const float *__restrict__ K, const float *__restrict__ V, size_t base, int key0,
-                                 int seq, int dim, int i, int g, UnitKV<DP> &kv) {
-    constexpr int NDB = DP / 16;
+__device__ inline void load_unit_k(const float *__restrict__ K, size_t base, int key0, int seq, int dim, int i,
+                                   int g, UnitKV<DP> &kv) {
     const size_t krow = size_t(min(key0 + i, seq - 1)) * dim;
 #pragma unroll
     for (int t = 0; t < UnitKV<DP>::kK; ++t) {
         const int d = min((DP / 4) * g + 4 * t, dim - 4);
         kv.k[t] = *reinterpret_cast<const f32x4 *>(K + base + krow + d);
     }
+}
+template <int DP>
+__device__ inline void load_unit_v(const float *__restrict__ V, size_t base, int key0, int seq, int dim, int i,
+                                   int g, UnitKV<DP> &kv) {
+    constexpr int NDB = DP / 16;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const size_t vrow = size_t(min(key0 + 4 * g + r, seq - 1)) * dim;
@@ -607,6 +613,16 @@ __device__ inline void load_unit(const float *__restrict__ K, const float *__res
             kv.v[r][e] = *reinterpret_cast<const f32x4 *>(V + base + vrow + d);
         }
     }
+}
+// Unconditional loads with row and column indices clamped into the tensors,
+// so the compiler waits for exactly the chunk it consumes. A clamped key row
+// only reaches masked scores (and P = 0 for V); a clamped dim of K meets a
+// zero in Q, and a clamped dim of V only reaches outputs that are not stored.
+template <int DP>
+__device__ inline void load_unit(const float *__restrict__ K, const float *__restrict__ V, size_t base, int key0,
+                                 int seq, int dim, int i, int g, UnitKV<DP> &kv) {
+    load_unit_k<DP>(K, base, key0, seq, dim, i, g, kv);
+    load_unit_v<DP>(V, base, key0, seq, dim, i, g, kv);
 }
 }  // namespace pairs
 
@@ -643,8 +659,10 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
     const size_t base = size_t(head) * size_t(seq) * size_t(dim);
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
-    // A chunk is up to CH units that are all shared or all xb-only.
-    auto chunk_end = [&](int t) { return min(u1, min(t + CH, t < uc ? uc : ub)); };
+    // A chunk is up to CH units that are all shared or all xb-only, inside
+    // the range [.., seg_end) the chunk loop is working on.
+    int seg_end = u1;
+    auto chunk_end = [&](int t) { return min(seg_end, min(t + CH, t < uc ? uc : ub)); };
     // Every chunk loads CH units; positions past the chunk's end re-read its
     // last unit and are never used.
     auto load_chunk = [&](KV(&buf)[CH], int t) {
@@ -738,11 +756,10 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
                             __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r], st.acc[b], 0, 0, 0);
             }
     };
-    // A whole shared chunk: both query blocks in one branch-free basic block,
-    // so the scheduler can overlap one block's softmax with the other's MFMAs.
-    // Masks are selects on a wave-uniform flag; the rescale is unconditional.
-    auto both_full = [&](const KV(&kv)[CH], int t) {
-        f32x4 s_a[CH], s_b[CH];
+    // Shared chunks: both query blocks' scores, the online softmax update and
+    // the P.V product, as separate steps so the pipelined loop below can put
+    // the next chunk's scores beside this chunk's softmax.
+    auto scores2 = [&](const KV(&kv)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) {
             s_a[c] = zero4;
@@ -753,51 +770,63 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
                 s_b[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qb[d], s_b[c], 0, 0, 0);
             }
         }
-        auto update = [&](f32x4(&s)[CH], int x, State &st) {
-            const int query = x * kUnit + i;
-            float tile_max = -INFINITY;
+    };
+    // Masks are selects on a wave-uniform flag (MASK false: the caller knows
+    // no key of the chunk is masked); the rescale is unconditional.
+    auto update = [&](f32x4(&s)[CH], int t, int x, State &st, auto mask) {
+        constexpr bool MASK = decltype(mask)::value;
+        const int query = x * kUnit + i;
+        float tile_max = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < CH; ++c) {
-                const int key0 = (t + c) * kUnit;
-                const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
+        for (int c = 0; c < CH; ++c) {
+            const int key0 = (t + c) * kUnit;
+            const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < 4; ++r) {
+                if (MASK) {
                     const int key = key0 + 4 * g + r;
                     const bool live = key < seq && (!CAUSAL || key <= query);
                     s[c][r] = (masked_unit && !live) ? -INFINITY : s[c][r];
-                    tile_max = fmaxf(tile_max, s[c][r]);
                 }
+                tile_max = fmaxf(tile_max, s[c][r]);
             }
-            tile_max = pairs::lanes_max(tile_max);
-            const float next_max = fmaxf(st.row_max, tile_max);
-            const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
-            float tile_sum = 0.f;
+        }
+        tile_max = pairs::lanes_max(tile_max);
+        const float next_max = fmaxf(st.row_max, tile_max);
+        const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
+        float tile_sum = 0.f;
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
+        for (int c = 0; c < CH; ++c)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - next_max);
-                    tile_sum += s[c][r];
-                }
-            st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
-            st.row_max = next_max;
+            for (int r = 0; r < 4; ++r) {
+                s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - next_max);
+                tile_sum += s[c][r];
+            }
+        st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
+        st.row_max = next_max;
 #pragma unroll
-            for (int b = 0; b < NDB; ++b) st.acc[b] *= old_weight;
-        };
-        auto pv = [&](const f32x4(&s)[CH], State &st) {
+        for (int b = 0; b < NDB; ++b) st.acc[b] *= old_weight;
+    };
+    auto pv = [&](const KV(&kv)[CH], const f32x4(&s)[CH], State &st) {
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
+        for (int c = 0; c < CH; ++c)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int b = 0; b < NDB; ++b)
-                        st.acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r],
-                                                                         st.acc[b], 0, 0, 0);
-        };
-        update(s_a, xa, sa);
-        update(s_b, xb, sb);
-        pv(s_a, sa);
-        pv(s_b, sb);
+                for (int b = 0; b < NDB; ++b)
+                    st.acc[b] =
+                        __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].v[r][b >> 2][b & 3], s[c][r], st.acc[b], 0, 0, 0);
+    };
+    // A whole shared chunk in one branch-free basic block for both query
+    // blocks, so the scheduler can overlap one block's softmax with the
+    // other's MFMAs.
+    auto both_full = [&](const KV(&kv)[CH], int t) {
+        f32x4 s_a[CH], s_b[CH];
+        scores2(kv, s_a, s_b);
+        update(s_a, t, xa, sa, std::true_type{});
+        update(s_b, t, xb, sb, std::true_type{});
+        pv(kv, s_a, sa);
+        pv(kv, s_b, sb);
     };
     auto process = [&](const KV(&kv)[CH], int t) {
         const int n = chunk_end(t) - t;
@@ -809,23 +838,166 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
         attend(kv, t, n, xb, qb, sb);
     };
 
-    // Two chunk buffers: the next chunk's loads are in flight while the
-    // current one is consumed (the last prefetch re-reads the last chunk).
+    // Runs of whole chunks with no masked key take a software pipeline:
+    // chunk c's scores are computed in step c-1, so in step c the MFMAs of
+    // chunk c+1's scores sit beside chunk c's softmax, then chunk c's P.V
+    // follows. K runs two chunks ahead of use, V one; each has two buffers.
+    // The step is one basic block whose MFMAs and VALU work are interleaved
+    // explicitly. Two runs qualify: shared units below xa's diagonal unit
+    // (both query blocks), and xb-only units below xb's diagonal unit (xb
+    // alone); both also end at the last whole unit of seq. What is left of
+    // [u0, u1) takes the chunk loop further down.
+    // The pipeline's loads are buffer loads: a per-lane byte offset fixed for
+    // the kernel plus the unit's row offset as a scalar, so a load costs no
+    // address arithmetic (a head's K and V must fit 2 GiB each).
+    const bool offsets_fit = size_t(seq) * size_t(dim) * 4u < (size_t(1) << 31);
+    auto steps_in = [&](int lo, int hi) { return offsets_fit && hi - lo >= 2 * CH ? (hi - lo) / CH : 0; };
+    const int whole = seq / kUnit;
+    const int n_two = steps_in(u0, min(u1, single ? 0 : (CAUSAL ? xa : whole)));  // wave-uniform
+    const int up = u0 + n_two * CH;
+    const int b_lo = max(u0, uc);
+    const int n_one = steps_in(b_lo, min(u1, CAUSAL ? xb : whole));  // wave-uniform
+    const int bp = b_lo + n_one * CH;
+
+    const uint32_t head_bytes = uint32_t(seq) * uint32_t(dim) * 4u, unit_bytes = kUnit * uint32_t(dim) * 4u;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(K + base), 0, int(head_bytes), int(kRawBuffer));
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(V + base), 0, int(head_bytes), int(kRawBuffer));
+    // Lane offsets inside a unit: K row i, dims (DP/4) g + 4 s; V rows
+    // 4 g + r, dims NDB i + 4 e (dims clamped as in load_unit).
+    uint32_t ok[KV::kK], ov[4][KV::kV];
+#pragma unroll
+    for (int s4 = 0; s4 < KV::kK; ++s4)
+        ok[s4] = (uint32_t(i) * uint32_t(dim) + uint32_t(min((DP / 4) * g + 4 * s4, dim - 4))) * 4u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < KV::kV; ++e)
+            ov[r][e] = (uint32_t(4 * g + r) * uint32_t(dim) + uint32_t(min(NDB * i + 4 * e, dim - 4))) * 4u;
+    auto load4 = [](__amdgpu_buffer_rsrc_t rsrc, uint32_t lane_offset, uint32_t unit_offset) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, int(lane_offset), int(unit_offset), 0);
+        return f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+    };
+    auto load_k = [&](KV(&buf)[CH], int t) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int s4 = 0; s4 < KV::kK; ++s4) buf[c].k[s4] = load4(rk, ok[s4], uint32_t(t + c) * unit_bytes);
+    };
+    auto load_v = [&](KV(&buf)[CH], int t) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int e = 0; e < KV::kV; ++e) buf[c].v[r][e] = load4(rv, ov[r][e], uint32_t(t + c) * unit_bytes);
+    };
+    // xb's scores alone, the chunk's units interleaved so that two MFMA
+    // chains alternate.
+    auto scores1 = [&](const KV(&kv)[CH], f32x4(&s_b)[CH]) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c) s_b[c] = zero4;
+#pragma unroll
+        for (int d = 0; d < D4; ++d)
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+                s_b[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qb[d], s_b[c], 0, 0, 0);
+    };
+    // `steps` chunks from unit p0, for both query blocks (TWO) or xb alone.
+    auto pipeline = [&](int p0, int steps, auto two) {
+        constexpr bool TWO = decltype(two)::value;
+        const int last = p0 + (steps - 1) * CH;  // first unit of the last chunk
+        auto scores = [&](const KV(&kv)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
+            if constexpr (TWO)
+                scores2(kv, s_a, s_b);
+            else
+                scores1(kv, s_b);
+        };
+        // Chunk t's softmax and P.V from its scores (s_a, s_b) and V.
+        auto consume = [&](int t, const KV(&vcur)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
+            if constexpr (TWO) update(s_a, t, xa, sa, std::false_type{});
+            update(s_b, t, xb, sb, std::false_type{});
+            if constexpr (TWO) pv(vcur, s_a, sa);
+            pv(vcur, s_b, sb);
+        };
+        KV kb0[CH], kb1[CH], vb0[CH], vb1[CH];
+        f32x4 sa0[CH], sb0[CH], sa1[CH], sb1[CH];
+        load_k(kb0, p0);
+        load_k(kb1, p0 + CH);
+        load_v(vb0, p0);
+        scores(kb0, sa0, sb0);
+        // Step for chunk t, not the last: scores in (s_a, s_b), V in vcur; the
+        // next chunk's K in knext, its scores into (n_a, n_b); kfree takes the
+        // K two chunks ahead and vnext the next chunk's V. Positions past the
+        // run re-read its last chunk and are never used.
+        auto step = [&](int t, KV(&kfree)[CH], const KV(&knext)[CH], const KV(&vcur)[CH], KV(&vnext)[CH],
+                        f32x4(&s_a)[CH], f32x4(&s_b)[CH], f32x4(&n_a)[CH], f32x4(&n_b)[CH]) {
+            load_k(kfree, min(t + 2 * CH, last));
+            load_v(vnext, min(t + CH, last));
+            if constexpr (TWO) update(s_a, t, xa, sa, std::false_type{});
+            update(s_b, t, xb, sb, std::false_type{});
+            scores(knext, n_a, n_b);
+            if constexpr (TWO) pv(vcur, s_a, sa);
+            pv(vcur, s_b, sb);
+            // CH D4 score MFMAs and 4 CH NDB P.V MFMAs per query block, CH DP/8
+            // vector loads; the softmax fills the MFMA shadow.
+            constexpr int kMfma = (TWO ? 2 : 1) * CH * (D4 + 4 * NDB), kLoads = CH * DP / 8;
+#pragma unroll
+            for (int j = 0; j < kLoads; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+            }
+#pragma unroll
+            for (int j = kLoads; j < kMfma; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+            // Nothing crosses into the next step: its scores wait on this
+            // step's loads.
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        // Two steps per iteration with no branch between them: a step's
+        // prefetch is consumed by the next step, and a block boundary there
+        // lets the compiler sink the loads to their use.
+        int t = p0, n = steps - 1;  // steps before the last
+        for (; n >= 2; n -= 2, t += 2 * CH) {
+            step(t, kb0, kb1, vb0, vb1, sa0, sb0, sa1, sb1);
+            step(t + CH, kb1, kb0, vb1, vb0, sa1, sb1, sa0, sb0);
+        }
+        if (n) {
+            step(t, kb0, kb1, vb0, vb1, sa0, sb0, sa1, sb1);
+            consume(t + CH, vb1, sa1, sb1);
+        } else {
+            consume(t, vb0, sa0, sb0);
+        }
+    };
+    if (n_two) pipeline(u0, n_two, std::true_type{});
+    if (n_one) pipeline(b_lo, n_one, std::false_type{});
+
+    // The rest: [up, b_lo) and [bp, u1) when the xb-only run was taken,
+    // [up, u1) otherwise. Two chunk buffers: the next chunk's loads are in
+    // flight while the current one is consumed (the last prefetch re-reads
+    // the last chunk).
     KV buf0[CH], buf1[CH];
-    if (u0 < u1) {
-        int t = u0;
+    for (int part = 0; part < 2; ++part) {
+        const int lo = part == 0 ? up : (n_one ? bp : u1);
+        seg_end = part == 0 && n_one ? b_lo : u1;
+        if (lo >= seg_end) continue;
+        int t = lo;
         load_chunk(buf0, t);
         for (;;) {
             int e = chunk_end(t);
-            load_chunk(buf1, e < u1 ? e : t);
+            load_chunk(buf1, e < seg_end ? e : t);
             process(buf0, t);
             t = e;
-            if (t >= u1) break;
+            if (t >= seg_end) break;
             e = chunk_end(t);
-            load_chunk(buf0, e < u1 ? e : t);
+            load_chunk(buf0, e < seg_end ? e : t);
             process(buf1, t);
             t = e;
-            if (t >= u1) break;
+            if (t >= seg_end) break;
         }
     }
 

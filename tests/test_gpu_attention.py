@@ -161,6 +161,10 @@ def test_split_key_grids(runtime, h, s, d, causal):
     (12, 700, 48, False),  # head dim padded to 64
     (16, 512, 128, True), (32, 256, 100, True),  # head dims 128 and 100 (padded to 128)
     (1, 4096, 64, True),  # one head, 128 blocks
+    # Noncausal odd block counts (the middle block alone runs the one-block
+    # pipeline), ragged and whole; long rows; head dims 128 and 96.
+    (8, 1000, 64, False), (6, 1008, 64, False), (8, 1008, 64, True), (2, 3000, 64, False),
+    (8, 1024, 128, False), (5, 1100, 96, False),
 ])
 def test_paired_small_grids(runtime, h, s, d, causal):
     # Grids that would otherwise split keys across blocks run 16-query waves
