@@ -561,7 +561,15 @@ size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t sl
 // Scores are in log2 units (Q pre-scaled by scale * log2(e)), as in the
 // flash kernel above.
 namespace pairs {
-constexpr int kWaves = 4, kThreads = 64 * kWaves;
+// Waves per block and units per chunk by padded head dim. A head-dim-64 wave
+// fits in 256 registers, so eight-wave blocks hold two waves per SIMD and one
+// wave's softmax runs beside the other's MFMAs (a wave's own VALU work does
+// not overlap its MFMAs); a head-dim-128 wave needs more and runs alone on
+// its SIMD in a four-wave block.
+template <int DP>
+struct Config {
+    static constexpr int kWaves = DP == 64 ? 8 : 4, kChunk = 1;
+};
 constexpr int kUnit = 16;  // keys per unit, queries per query block
 constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
 
@@ -628,8 +636,8 @@ __device__ inline void load_unit(const float *__restrict__ K, const float *__res
 
 // Grid: heads * ceil(X / 2) blocks, block b = pair b / heads of head b % heads.
 // Needs dim % 4 == 0 and 16-byte aligned tensors (vector loads), dim <= DP.
-template <int DP, bool CAUSAL, int CH>
-__global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const float *__restrict__ Q,
+template <int DP, bool CAUSAL, int CH, int NW>
+__global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__restrict__ Q,
                                                                         const float *__restrict__ K,
                                                                         const float *__restrict__ V,
                                                                         float *__restrict__ O, int seq, int dim,
@@ -637,8 +645,8 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
     using namespace pairs;
     using KV = UnitKV<DP>;
     constexpr int D4 = DP / 4, NDB = DP / 16;
-    __shared__ f32x4 part[kWaves * 2][kUnit][D4];  // DP floats per query row
-    __shared__ float2 mls[kWaves * 2][kUnit];
+    __shared__ f32x4 part[NW * 2][kUnit][D4];  // DP floats per query row
+    __shared__ float2 mls[NW * 2][kUnit];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);  // uniform: scalar loop control
@@ -655,7 +663,7 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
     // takes the units between the w-th and (w+1)-th quarter of the cost.
     const int cost = 2 * uc + (ub - uc);
     auto unit_at = [&](int c) { return c <= 2 * uc ? (c + 1) / 2 : c - uc; };
-    const int u0 = unit_at(cost * wave / kWaves), u1 = unit_at(cost * (wave + 1) / kWaves);
+    const int u0 = unit_at(cost * wave / NW), u1 = unit_at(cost * (wave + 1) / NW);
     const size_t base = size_t(head) * size_t(seq) * size_t(dim);
     const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
 
@@ -1020,7 +1028,7 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
 
     // Merge: thread -> (query block, query, 4 dims). With a single query
     // block, slot 1 of every wave holds it.
-    for (int o = int(threadIdx.x); o < 2 * kUnit * D4; o += kThreads) {
+    for (int o = int(threadIdx.x); o < 2 * kUnit * D4; o += NW * 64) {
         const int seg = o / (kUnit * D4), rest = o % (kUnit * D4);
         const int qi = rest / D4, d4 = rest % D4;
         if (seg == 0 && single) continue;
@@ -1028,11 +1036,11 @@ __global__ __launch_bounds__(pairs::kThreads) void attention_pairs_mfma(const fl
         if (q >= seq || d >= dim) continue;
         float top = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) top = fmaxf(top, mls[w * 2 + seg][qi].x);
+        for (int w = 0; w < NW; ++w) top = fmaxf(top, mls[w * 2 + seg][qi].x);
         f32x4 num = zero4;
         float den = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float2 ml = mls[w * 2 + seg][qi];
             const float wt = __builtin_amdgcn_exp2f(ml.x - top);
             den = fmaf(wt, ml.y, den);
@@ -1073,17 +1081,18 @@ bool use_pairs(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
            pair_blocks(heads, seq) >= kPairsMinBlocks;
 }
 
-template <int DP, int CH>
+template <int DP>
 hipError_t launch_pairs(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                         uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    using C = pairs::Config<DP>;
     const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
-    const dim3 grid(pair_blocks(heads, seq)), block(pairs::kThreads);
+    const dim3 grid(pair_blocks(heads, seq)), block(C::kWaves * 64);
     if (causal)
-        hipLaunchKernelGGL((attention_pairs_mfma<DP, true, CH>), grid, block, 0, stream, q, k, v, out, int(seq),
-                           int(dim), qscale, int(heads));
+        hipLaunchKernelGGL((attention_pairs_mfma<DP, true, C::kChunk, C::kWaves>), grid, block, 0, stream, q, k, v,
+                           out, int(seq), int(dim), qscale, int(heads));
     else
-        hipLaunchKernelGGL((attention_pairs_mfma<DP, false, CH>), grid, block, 0, stream, q, k, v, out, int(seq),
-                           int(dim), qscale, int(heads));
+        hipLaunchKernelGGL((attention_pairs_mfma<DP, false, C::kChunk, C::kWaves>), grid, block, 0, stream, q, k, v,
+                           out, int(seq), int(dim), qscale, int(heads));
     return hipGetLastError();
 }
 
@@ -1092,7 +1101,7 @@ hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, cons
                         float *workspace, uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
     if constexpr (DP >= 64) {
         if (vec && use_pairs(heads, seq, dim, causal))
-            return launch_pairs<DP, DP == 64 ? 2 : 1>(stream, q, k, v, out, heads, seq, dim, causal);
+            return launch_pairs<DP>(stream, q, k, v, out, heads, seq, dim, causal);
     }
     const SplitPlan plan = split_plan(heads, seq, causal);
     if (plan.slices > 1) {
@@ -1119,6 +1128,8 @@ hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, cons
                   : launch_online<DP, 4, false, false>(stream, q, k, v, out, nullptr, heads, seq, dim, whole, vec);
 }
 
+int pairs_waves(int dp) { return dp == 64 ? pairs::Config<64>::kWaves : pairs::Config<128>::kWaves; }
+
 template <int DP>
 uint32_t lds_bytes(int nw) {
     return nw == 8 ? AttnShape<DP, 8>::kLdsBytes : AttnShape<DP, 4>::kLdsBytes;
@@ -1131,8 +1142,8 @@ LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, b
     if (use_pairs(heads, seq, dim, causal))
         return {dp == 64 ? "attention_online_mfma16_d64_pairs" : "attention_online_mfma16_d128_pairs",
                 {pair_blocks(heads, seq), 1, 1},
-                {uint32_t(pairs::kThreads), 1, 1},
-                uint32_t(pairs::kWaves * 2 * pairs::kUnit * (dp * sizeof(float) + sizeof(float2)))};
+                {uint32_t(pairs_waves(dp) * 64), 1, 1},
+                uint32_t(pairs_waves(dp) * 2 * pairs::kUnit * (dp * sizeof(float) + sizeof(float2)))};
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
     const SplitPlan plan = split_plan(heads, seq, causal);
