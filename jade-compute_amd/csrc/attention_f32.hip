@@ -534,15 +534,15 @@ size_t split_part_floats(uint32_t heads, uint32_t seq, uint32_t dim, uint32_t sl
 }
 
 // ---- Small grids: 16-query waves splitting keys inside the block -----------
-// For grids whose 128-query blocks cannot fill the chip. A block of four waves
-// owns two 16-query blocks of one head, x and X-1-x (X = ceil(seq/16); one
-// block where the two coincide), so every block does the same work under the
-// causal mask: x+1 and X-x 16-key units, X+1 in all (2X without the mask).
-// The block's units (those of x, then those of the partner) are cut into four
-// equal runs, one per wave; a wave whose run crosses from one query block into
-// the other switches queries there. Each wave loads its own K and V rows from
-// global memory (L2) straight into registers in MFMA operand order, one chunk
-// of units ahead, so the K loop has no LDS staging and no barrier. At the end
+// For grids whose 128-query blocks cannot fill the chip. A block of NW waves
+// (eight for head dim 64, four for 128) owns two 16-query blocks of one head,
+// x and X-1-x (X = ceil(seq/16); one block where the two coincide), so every
+// block does the same work under the causal mask: x+1 and X-x 16-key units,
+// X+1 in all (2X without the mask). A unit that serves both query blocks
+// costs two, one that serves only X-1-x costs one; the block's units are cut
+// into NW runs of equal cost, one per wave. Each wave loads its own K and V
+// rows from global memory (L2) straight into registers in MFMA operand order,
+// ahead of use, so the K loop has no LDS staging and no barrier. At the end
 // the waves merge their partial (O, max, normaliser) rows through LDS and
 // store O: no second launch and no workspace.
 //
