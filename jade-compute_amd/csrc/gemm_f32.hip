@@ -1020,18 +1020,27 @@ struct Slice {
     float b[16];  // B[k0 + 16h + s][col c] at b[s]
 };
 
-// Aligned rows (K % 4 == 0): a 4-float run clamped to start at most at
-// K - 4 stays inside its row. Unaligned rows (BUFA): buffer loads at
+// BUFA (A below 2 GiB; required when K % 4 != 0): buffer loads at
 // 4-byte-aligned offsets, unclamped: a run that crosses the end of its row
-// reads the next row's first floats at k >= K (zeroed when consumed), and
-// the buffer's range check returns zero past the end of A.
-template <bool BUFA>
+// reads the next row's first floats at k >= K (zeroed when consumed), and the
+// buffer's range check returns zero past the end of A. Otherwise a 4-float
+// run clamped to start at most at K - 4 stays inside its (aligned) row.
+//
+// BUFB (K*N*4 < 2^31): B through buffer loads at a 32-bit offset per lane, one
+// add per load instead of a clamped 64-bit address; rows k >= K lie past the
+// buffer's end and read as zero.
+//
+// `live` false (a prefetch past the wave's last slice): buffer loads go to an
+// offset past any buffer of this kernel, which reads zero without touching
+// memory, so the kernel does not end waiting on loads nobody consumes.
+constexpr uint32_t kDeadOffset = 0x80000000u;
+template <bool BUFA, bool BUFB>
 __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_rsrc_t ra,
-                                  const float *__restrict__ B, int K, int N, size_t arow, int lda, int bcol, int k0,
-                                  int h, Slice &s) {
+                                  const float *__restrict__ B, __amdgpu_buffer_rsrc_t rb, int K, int N, size_t arow,
+                                  int lda, int bcol, int k0, bool live, int h, Slice &s) {
     const int kb = k0 + 16 * h;
     if constexpr (BUFA) {
-        const uint32_t first = (uint32_t(arow) * uint32_t(lda) + uint32_t(kb)) * 4u;
+        const uint32_t first = live ? (uint32_t(arow) * uint32_t(lda) + uint32_t(kb)) * 4u : kDeadOffset;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(ra, int(first + 16u * q), 0, 0);
@@ -1042,11 +1051,21 @@ __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_r
 #pragma unroll
         for (int q = 0; q < 4; ++q) s.a[q] = *reinterpret_cast<const f32x4 *>(ap + min(kb + 4 * q, K - 4));
     }
+    if constexpr (BUFB) {
+        const uint32_t first = live ? (uint32_t(kb) * uint32_t(N) + uint32_t(bcol)) * 4u : kDeadOffset;
+        const uint32_t row = uint32_t(N) * 4u;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s.b[e] = B[size_t(min(kb + e, K - 1)) * N + bcol];
+        for (int e = 0; e < 16; ++e)
+            s.b[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(first + uint32_t(e) * row), 0, 0));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s.b[e] = B[size_t(min(kb + e, K - 1)) * N + bcol];
+    }
 }
 
-// `valid` = K - (k0 + 16h): operand pairs at s >= valid lie past K.
+// `valid` = K - (k0 + 16h): operand pairs at s >= valid lie past K. ZB: B is
+// already zero there (buffer loads), so only A is masked.
+template <bool ZB>
 __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
     f32x16 part;
 #pragma unroll
@@ -1056,7 +1075,7 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
-            const float a = i < valid ? s.a[q][e] : 0.f, b = i < valid ? s.b[i] : 0.f;
+            const float a = i < valid ? s.a[q][e] : 0.f, b = ZB || i < valid ? s.b[i] : 0.f;
             part = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, part, 0, 0, 0);
         }
     acc += part;
@@ -1066,21 +1085,25 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 // gridDim.y > 1: a batch of independent products, product z at A + z*sa,
 // B + z*sb, C + z*sc (attention's P.V per head, or the K slices of a split
 // product: sa = K, sb = K*N with A rows lda apart).
-// BUFA: A rows are not 16-byte aligned (K % 4 != 0); A is read through buffer
-// loads, which needs M*K*4 < 2^31 and no batch (lda = K).
-template <int G, bool BUFA = false>
+// BUFA: A is read through buffer loads, which needs ((M-1)*lda + K)*4 < 2^31
+// (per product of a batch); unaligned rows (K % 4 != 0) require it. BUFB: B
+// is read through buffer loads (K*N*4 < 2^31; per product of a batch).
+template <int G, bool BUFA, bool BUFB>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
                                                           float *__restrict__ C, int M, int N, int K, int lda,
-                                                          int tiles_m, int tiles_n, size_t sa = 0, size_t sb = 0,
-                                                          size_t sc = 0) {
+                                                          int tiles_m, int tiles_n, size_t sa, size_t sb,
+                                                          size_t sc) {
     using namespace direct;
     constexpr int D = kDepth;
-    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(A), 0, BUFA ? int(uint32_t(M) * uint32_t(K) * 4u) : 0, int(kBufferWord3));
     __shared__ float red[(G > 1 ? G - 1 : 1) * 16 * 64];
     A += blockIdx.y * sa;
     B += blockIdx.y * sb;
     C += blockIdx.y * sc;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(A), 0, BUFA ? int((uint32_t(M - 1) * uint32_t(lda) + uint32_t(K)) * 4u) : 0,
+        int(kBufferWord3));
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(B), 0, BUFB ? int(uint32_t(K) * uint32_t(N) * 4u) : 0, int(kBufferWord3));
     int tm, tn;
     tile_coords(tiles_m, tiles_n, tm, tn);
     const int lane = threadIdx.x & 63;
@@ -1092,7 +1115,8 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
     const int slices = (K + kBK - 1) / kBK;
     const int count = g < slices ? (slices - g + G - 1) / G : 0;  // this wave's slices g, g+G, ...
     // K offset of this wave's j-th slice, clamped to the last slice: loads past
-    // the end re-read an in-range slice and are never consumed.
+    // the end (dead: buffer loads skip them) re-read an in-range slice and are
+    // never consumed.
     auto slice_k = [&](int j) { return min(g + j * G, slices - 1) * kBK; };
     auto valid = [&](int j) { return K - slice_k(j) - 16 * h; };
     f32x16 acc;
@@ -1102,15 +1126,16 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
     if (count > 0) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            load_slice<BUFA>(A, ra, B, K, N, arow, lda, bcol, slice_k(d), h, buf[d]);
+            load_slice<BUFA, BUFB>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(d), d < count, h, buf[d]);
             __builtin_amdgcn_sched_barrier(0);  // loads issued slice by slice
         }
         int i = 0;
         for (; i + D <= count; i += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                mma_slice(buf[d], valid(i + d), acc);
-                load_slice<BUFA>(A, ra, B, K, N, arow, lda, bcol, slice_k(i + d + D), h, buf[d]);
+                mma_slice<BUFB>(buf[d], valid(i + d), acc);
+                load_slice<BUFA, BUFB>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(i + d + D), i + d + D < count,
+                                       h, buf[d]);
                 // Keep the slices in order: interleaving their independent
                 // MFMA chains would make the first one wait for every load.
                 __builtin_amdgcn_sched_barrier(0);
@@ -1118,7 +1143,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         }
 #pragma unroll
         for (int d = 0; d < D; ++d)
-            if (i + d < count) mma_slice(buf[d], valid(i + d), acc);
+            if (i + d < count) mma_slice<BUFB>(buf[d], valid(i + d), acc);
     }
     if (G > 1) {
         if (g > 0) {
@@ -1137,6 +1162,38 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         const int crow = tm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
         if (crow < M && col < N) C[size_t(crow) * N + col] = acc[v];
     }
+}
+
+// One direct launch of G waves per 32x32 tile; A and B through buffer loads
+// when a product's operand is below 2 GiB (A always when `bufa`: unaligned
+// rows, whose limit the caller checks).
+template <int G>
+void launch_direct_g(hipStream_t stream, dim3 grid, bool bufa, const float *a, const float *b, float *c, int m,
+                     int n, int k, int lda, int tiles_m, int tiles_n, size_t sa, size_t sb, size_t sc) {
+    const bool bufb = uint64_t(k) * uint64_t(n) * 4u < (uint64_t(1) << 31);
+    bufa = bufa || (uint64_t(m - 1) * uint64_t(lda) + uint64_t(k)) * 4u < (uint64_t(1) << 31);
+    const dim3 block(64 * G);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
+    };
+    if (bufa)
+        bufb ? go(gemm_f32_direct<G, true, true>) : go(gemm_f32_direct<G, true, false>);
+    else
+        bufb ? go(gemm_f32_direct<G, false, true>) : go(gemm_f32_direct<G, false, false>);
+}
+
+hipError_t launch_direct(hipStream_t stream, dim3 grid, int g, bool bufa, const float *a, const float *b, float *c,
+                         int m, int n, int k, int lda, int tiles_m, int tiles_n, size_t sa = 0, size_t sb = 0,
+                         size_t sc = 0) {
+    if (g == 4)
+        launch_direct_g<4>(stream, grid, bufa, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
+    else if (g == 2)
+        launch_direct_g<2>(stream, grid, bufa, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
+    else if (g == 1)
+        launch_direct_g<1>(stream, grid, bufa, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
 }
 
 // C[i] = sum over slices z (in order) of W[z*MN + i].
@@ -1610,10 +1667,8 @@ hipError_t gemm_f32_batched_direct(hipStream_t stream, const float *a, const flo
                                    uint32_t n, uint32_t k, uint32_t batch, size_t sa, size_t sb, size_t sc) {
     if (k % 4 != 0 || ((reinterpret_cast<uintptr_t>(a) | sa * sizeof(float)) & 15u) != 0) return hipErrorInvalidValue;
     const int tiles_m = int((m + 31) / 32), tiles_n = int((n + 31) / 32);
-    const dim3 grid(unsigned(tiles_m * tiles_n), batch), block(256);
-    hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k), tiles_m, tiles_n, sa,
-                       sb, sc);
-    return hipGetLastError();
+    return launch_direct(stream, dim3(unsigned(tiles_m * tiles_n), batch), 4, false, a, b, c, int(m), int(n), int(k),
+                         int(k), tiles_m, tiles_n, sa, sb, sc);
 }
 
 hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n,
@@ -1640,39 +1695,21 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
         return hipGetLastError();
     }
     if (p.direct) {
-        const dim3 grid(unsigned(p.tiles_m * p.tiles_n)), block(unsigned(64 * p.direct));
+        const dim3 grid(unsigned(p.tiles_m * p.tiles_n));
         if (p.slices > 1) {
             // K slices of p.kchunk (which divides K) as a batch of products
             // into the workspace, then the ordered reduce.
             const size_t mn = size_t(m) * n;
-            hipLaunchKernelGGL(gemm_f32_direct<4>, dim3(grid.x, unsigned(p.slices)), block, 0, stream, a, b, workspace,
-                               int(m), int(n), p.kchunk, int(k), p.tiles_m, p.tiles_n, size_t(p.kchunk),
-                               size_t(p.kchunk) * n, mn);
-            const hipError_t status = hipGetLastError();
+            const hipError_t status =
+                launch_direct(stream, dim3(grid.x, unsigned(p.slices)), 4, false, a, b, workspace, int(m), int(n),
+                              p.kchunk, int(k), p.tiles_m, p.tiles_n, size_t(p.kchunk), size_t(p.kchunk) * n, mn);
             if (status != hipSuccess) return status;
             hipLaunchKernelGGL(splitk_reduce, dim3(unsigned((mn + 1023) / 1024)), dim3(256), 0, stream, workspace, c, mn,
                                p.slices);
-        } else if (p.bufa) {
-            if (p.direct == 4)
-                hipLaunchKernelGGL((gemm_f32_direct<4, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
-                                   int(k), p.tiles_m, p.tiles_n);
-            else if (p.direct == 2)
-                hipLaunchKernelGGL((gemm_f32_direct<2, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
-                                   int(k), p.tiles_m, p.tiles_n);
-            else
-                hipLaunchKernelGGL((gemm_f32_direct<1, true>), grid, block, 0, stream, a, b, c, int(m), int(n), int(k),
-                                   int(k), p.tiles_m, p.tiles_n);
-        } else if (p.direct == 4) {
-            hipLaunchKernelGGL(gemm_f32_direct<4>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
-                               p.tiles_m, p.tiles_n);
-        } else if (p.direct == 2) {
-            hipLaunchKernelGGL(gemm_f32_direct<2>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
-                               p.tiles_m, p.tiles_n);
-        } else {
-            hipLaunchKernelGGL(gemm_f32_direct<1>, grid, block, 0, stream, a, b, c, int(m), int(n), int(k), int(k),
-                               p.tiles_m, p.tiles_n);
+            return hipGetLastError();
         }
-        return hipGetLastError();
+        return launch_direct(stream, grid, p.direct, p.bufa, a, b, c, int(m), int(n), int(k), int(k), p.tiles_m,
+                             p.tiles_n);
     }
     float *out = p.slices > 1 ? workspace : c;
     const hipError_t status = launch_route_tiles(stream, r, a, b, out, m, n, k);
