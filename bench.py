@@ -141,16 +141,18 @@ def traffic_from_profiles(symbol_prefix, launch):
     path = os.path.join(PROFILE_DIR, "traffic.json")
     if not os.path.exists(path):
         return None
-    items = launch["grid"][0] * launch["grid"][1] * launch["grid"][2] * launch["block"][0]
+    block = launch["block"][0]
+    items = launch["grid"][0] * launch["grid"][1] * launch["grid"][2] * block
     try:
         table = json.load(open(path))
     except (OSError, ValueError):
         return None
-    for key, entry in table.items():
-        name, _, grid = key.rpartition("@")
-        if name.startswith(symbol_prefix) and grid == str(items):
-            return entry.get("bytes_per_launch")
-    return None
+    # Keys are "symbol@work-items@workgroup"; one symbol prefix can name
+    # several instantiations, so an ambiguous match gives no figure.
+    found = [entry.get("bytes_per_launch") for key, entry in table.items()
+             if len(key.split("@")) == 3 and key.split("@")[0].startswith(symbol_prefix)
+             and key.split("@")[1:] == [str(items), str(block)]]
+    return found[0] if len(found) == 1 else None
 
 
 class Prepared:
@@ -416,7 +418,7 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
             for row in _read_csv(path):
                 if row.get("Counter_Name") != counter:
                     continue
-                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
+                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]))
                 counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
     lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us |",
              "|---|---|---|---|---|---|---|"]
@@ -434,16 +436,18 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
             scale[counter] = expected_kib / measured if measured and np.isfinite(measured) else np.nan
         lines += ["", f"HBM counter calibration (copy_stream, {COPY_ELEMENTS * 4 / 2**20:.0f} MiB in and out): "
                       f"scale FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, WRITE_SIZE x{scale['WRITE_SIZE']:.4f}", "",
-                  "| kernel | grid (work-items) | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB/launch |",
-                  "|---|---|---|---|---|---|"]
+                  "| kernel | grid (work-items) | block | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB/launch |",
+                  "|---|---|---|---|---|---|---|"]
         for key, vals in sorted(counters.items()):
             fetch = np.mean(vals.get("FETCH_SIZE", [np.nan]))
             write = np.mean(vals.get("WRITE_SIZE", [np.nan]))
             nbytes = (fetch * scale["FETCH_SIZE"] + write * scale["WRITE_SIZE"]) * 1024.0
             count = max(len(vals.get("FETCH_SIZE", [])), len(vals.get("WRITE_SIZE", [])))
-            lines.append(f"| {key[0]} | {key[1]} | {count} | {fetch:.0f} | {write:.0f} | {nbytes / 1e6:.1f} |")
+            lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {count} | {fetch:.0f} | {write:.0f} | "
+                         f"{nbytes / 1e6:.1f} |")
             if np.isfinite(nbytes):
-                traffic[f"{key[0]}@{key[1]}"] = {"bytes_per_launch": nbytes, "fetch_kib": fetch, "write_kib": write}
+                traffic[f"{key[0]}@{key[1]}@{key[2]}"] = {"bytes_per_launch": nbytes, "fetch_kib": fetch,
+                                                          "write_kib": write}
     return "\n".join(lines), traffic
 
 
@@ -480,10 +484,11 @@ def summarize_mfma(directory):
     vals = {}
     for path in _find_all(directory, "counter_collection.csv"):
         for row in _read_csv(path):
-            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]))
+            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]))
             vals.setdefault(key, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
-    lines = ["| kernel | grid (work-items) | dispatches | GRBM_GUI_ACTIVE / XCD | SQ_VALU_MFMA_BUSY_CYCLES | MFMA busy |",
-             "|---|---|---|---|---|---|"]
+    lines = ["| kernel | grid (work-items) | block | dispatches | GRBM_GUI_ACTIVE / XCD | SQ_VALU_MFMA_BUSY_CYCLES "
+             "| MFMA busy |",
+             "|---|---|---|---|---|---|---|"]
     for key, v in sorted(vals.items()):
         if "SQ_VALU_MFMA_BUSY_CYCLES" not in v or "GRBM_GUI_ACTIVE" not in v:
             continue
@@ -492,8 +497,35 @@ def summarize_mfma(directory):
         if busy <= 0:
             continue
         flag = " (saturated)" if busy >= 2.0 ** 31 else ""
-        lines.append(f"| {key[0]} | {key[1]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | {busy:.4g}{flag} | "
+        lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | {busy:.4g}{flag} | "
                      f"{100.0 * busy / (gui * SIMDS):.1f}% |")
+    return "\n".join(lines)
+
+
+def summarize_counters(directory, match=""):
+    """Median per dispatch of every counter of a rocprofv3 --pmc run, per
+    (kernel, grid, workgroup) whose symbol contains `match`; SQ wave counters
+    also per wave (grid / 64 waves). Dispatches seen fewer than 10 times are
+    left out (set-up copies and fills)."""
+    vals = {}
+    for path in _find_all(directory, "counter_collection.csv"):
+        for row in _read_csv(path):
+            name = _short(row["Kernel_Name"])
+            if match not in name:
+                continue
+            key = (name, int(row["Grid_Size"]), int(row["Workgroup_Size"]))
+            per = vals.setdefault(key, {}).setdefault(row["Counter_Name"], {})
+            per[row["Dispatch_Id"]] = per.get(row["Dispatch_Id"], 0.0) + float(row["Counter_Value"])
+    lines = ["| kernel | grid (work-items) | block | dispatches | counter | median per dispatch | per wave |",
+             "|---|---|---|---|---|---|---|"]
+    for key, counters in sorted(vals.items()):
+        waves = key[1] // 64
+        for counter, per in sorted(counters.items()):
+            if len(per) < 10:
+                continue
+            median = float(np.median(list(per.values())))
+            per_wave = f"{median / waves:.1f}" if counter.startswith("SQ_") else ""
+            lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {len(per)} | {counter} | {median:.6g} | {per_wave} |")
     return "\n".join(lines)
 
 
@@ -583,7 +615,14 @@ def main():
     ap.add_argument("--summarize-mfma", metavar="PMC_DIR",
                     help="print MFMA busy shares from a rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE "
                          "output directory and exit")
+    ap.add_argument("--summarize-counters", metavar="PMC_DIR",
+                    help="print the median of every counter per kernel from a rocprofv3 --pmc output directory "
+                         "and exit (--match: only kernels whose symbol contains this text)")
+    ap.add_argument("--match", default="")
     args = ap.parse_args()
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters, args.match))
+        return
     if args.summarize_mfma:
         print(summarize_mfma(args.summarize_mfma))
         return

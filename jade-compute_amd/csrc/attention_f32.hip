@@ -645,7 +645,10 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     using namespace pairs;
     using KV = UnitKV<DP>;
     constexpr int D4 = DP / 4, NDB = DP / 16;
-    __shared__ f32x4 part[NW * 2][kUnit][D4];  // DP floats per query row
+    // DP floats per query row, rows padded by 16 bytes: the flush's lanes
+    // (query i, group g) write rows 16i + ... apart, which unpadded would put
+    // sixteen lanes on the same LDS banks.
+    __shared__ f32x4 part[NW * 2][kUnit][D4 + 1];
     __shared__ float2 mls[NW * 2][kUnit];
 
     const int lane = threadIdx.x & 63;
@@ -1143,7 +1146,7 @@ LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, b
         return {dp == 64 ? "attention_online_mfma16_d64_pairs" : "attention_online_mfma16_d128_pairs",
                 {pair_blocks(heads, seq), 1, 1},
                 {uint32_t(pairs_waves(dp) * 64), 1, 1},
-                uint32_t(pairs_waves(dp) * 2 * pairs::kUnit * (dp * sizeof(float) + sizeof(float2)))};
+                uint32_t(pairs_waves(dp) * 2 * pairs::kUnit * ((dp + 4) * sizeof(float) + sizeof(float2)))};
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
     const SplitPlan plan = split_plan(heads, seq, causal);

@@ -1,0 +1,82 @@
+"""bench.py's rocprofv3 summaries, on synthetic profiler CSVs (CPU only): the
+HBM counter calibration against the copy kernel, the per-(kernel, grid,
+workgroup) traffic table, and the lookup that fills the bench line's
+`roofline.traffic`."""
+import csv
+import importlib.util
+import os
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+@pytest.fixture(scope="module")
+def bench():
+    spec = importlib.util.spec_from_file_location("bench_under_test", os.path.join(ROOT, "bench.py"))
+    module = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(module)
+    return module
+
+
+def write_csv(path, rows):
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w", newline="") as f:
+        writer = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+        writer.writeheader()
+        writer.writerows(rows)
+
+
+SYMBOL = "void jade::hipk::(anonymous namespace)::{}(float const*, float*)"
+# Two instantiations with the same work-item count (1024x256 and 256x1024),
+# as the 4096^3 and 1024^3 GEMM launches have.
+KERNELS = [("copy_stream", 16777216, 256), ("gemm_f32_mfma<2, 2, true, 1, 1>", 262144, 256),
+           ("gemm_f32_mfma<1, 1, true, 1, 4>", 262144, 1024)]
+
+
+def make_profile(bench, tmp_path):
+    trace, fetch, write = [], [], []
+    copy_kib = bench.COPY_ELEMENTS * 4 / 1024.0
+    # Counter readings: the copy reads half and writes its true size, so the
+    # calibration scales FETCH_SIZE by 2 and WRITE_SIZE by 1.
+    readings = {"copy_stream": (copy_kib / 2, copy_kib), "gemm_f32_mfma<2, 2, true, 1, 1>": (1000.0, 500.0),
+                "gemm_f32_mfma<1, 1, true, 1, 4>": (100.0, 50.0)}
+    for dispatch, (name, items, block) in enumerate(KERNELS * 2):
+        full = SYMBOL.format(name)
+        trace.append({"Kernel_Name": full, "Grid_Size_X": items // block, "Grid_Size_Y": 1, "Grid_Size_Z": 1,
+                      "Workgroup_Size_X": block, "Start_Timestamp": 1000, "End_Timestamp": 3000 + dispatch})
+        for rows, counter, value in ((fetch, "FETCH_SIZE", readings[name][0]),
+                                     (write, "WRITE_SIZE", readings[name][1])):
+            rows.append({"Dispatch_Id": dispatch, "Kernel_Name": full, "Grid_Size": items, "Workgroup_Size": block,
+                         "Counter_Name": counter, "Counter_Value": value})
+    write_csv(str(tmp_path / "trace" / "run_kernel_trace.csv"), trace)
+    write_csv(str(tmp_path / "fetch" / "w" / "run_counter_collection.csv"), fetch)
+    write_csv(str(tmp_path / "write" / "w" / "run_counter_collection.csv"), write)
+    return bench.summarize_rocprof(str(tmp_path / "trace"), str(tmp_path / "fetch"), str(tmp_path / "write"))
+
+
+def test_traffic_table_is_keyed_by_workgroup_and_calibrated(bench, tmp_path):
+    text, traffic = make_profile(bench, tmp_path)
+    assert "scale FETCH_SIZE x2.0000, WRITE_SIZE x1.0000" in text
+    assert set(traffic) == {"copy_stream@16777216@256", "gemm_f32_mfma<2, 2, true, 1, 1>@262144@256",
+                            "gemm_f32_mfma<1, 1, true, 1, 4>@262144@1024"}
+    assert traffic["gemm_f32_mfma<2, 2, true, 1, 1>@262144@256"]["bytes_per_launch"] == pytest.approx(
+        (1000.0 * 2 + 500.0) * 1024)
+    assert traffic["copy_stream@16777216@256"]["bytes_per_launch"] == pytest.approx(2 * bench.COPY_ELEMENTS * 4)
+
+
+def test_traffic_lookup_picks_the_launched_instantiation(bench, tmp_path, monkeypatch):
+    _, traffic = make_profile(bench, tmp_path)
+    import json
+
+    (tmp_path / "profiles").mkdir()
+    (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(traffic))
+    monkeypatch.setattr(bench, "PROFILE_DIR", str(tmp_path / "profiles"))
+    big = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]})
+    small = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [256, 1, 1], "block": [1024, 1, 1]})
+    assert big == pytest.approx(2500.0 * 1024) and small == pytest.approx(250.0 * 1024)
+    # No entry, or a prefix that names two instantiations of one launch shape: no figure.
+    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [7, 1, 1], "block": [256, 1, 1]}) is None
+    traffic["gemm_f32_mfma<9, 9, true, 1, 1>@262144@256"] = {"bytes_per_launch": 1.0}
+    (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(traffic))
+    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}) is None
