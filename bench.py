@@ -85,7 +85,10 @@ class Workload:
         if warmup:
             self.rt.execute(self.jobs, warmup)
 
-    def preheat(self, target_ms=PREHEAT_MS):
+    def preheat(self, target_ms=None):
+        # The module-level PREHEAT_MS is read at call time: --preheat-ms
+        # replaces it after this class is defined.
+        target_ms = PREHEAT_MS if target_ms is None else target_ms
         batch = 1
         while self.preheat_ms < target_ms:
             ex = self.rt.execute(self.jobs, batch)

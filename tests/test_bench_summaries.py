@@ -1,7 +1,7 @@
-"""bench.py's rocprofv3 summaries, on synthetic profiler CSVs (CPU only): the
-HBM counter calibration against the copy kernel, the per-(kernel, grid,
-workgroup) traffic table, and the lookup that fills the bench line's
-`roofline.traffic`."""
+"""bench.py's harness on the CPU: its rocprofv3 summaries on synthetic
+profiler CSVs (the HBM counter calibration against the copy kernel, the
+per-(kernel, grid, workgroup) traffic table, the lookup that fills the bench
+line's `roofline.traffic`) and the time-based pre-heat on a stand-in runtime."""
 import csv
 import importlib.util
 import os
@@ -80,3 +80,27 @@ def test_traffic_lookup_picks_the_launched_instantiation(bench, tmp_path, monkey
     traffic["gemm_f32_mfma<9, 9, true, 1, 1>@262144@256"] = {"bytes_per_launch": 1.0}
     (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(traffic))
     assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}) is None
+
+
+def test_preheat_follows_the_command_line_value(bench, monkeypatch):
+    # --preheat-ms replaces the module-level PREHEAT_MS after the classes are
+    # defined; the pre-heat must read it when it runs.
+    class Execution:
+        gpu_ms, host_ms = 1.5, 1.5
+
+    class FakeRuntime:
+        def __init__(self):
+            self.calls = []
+
+        def execute(self, jobs, repeats):
+            self.calls.append(repeats)
+            result = Execution()
+            result.gpu_ms = 1.5 * repeats
+            return result
+
+    for target, want_calls in ((0.0, []), (10.0, [1, 2, 4])):
+        monkeypatch.setattr(bench, "PREHEAT_MS", target)
+        rt = FakeRuntime()
+        work = bench.Workload(rt, [], 1)
+        work.preheat()
+        assert rt.calls == want_calls and work.preheat_ms >= target
