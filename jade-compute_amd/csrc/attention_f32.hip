@@ -1076,12 +1076,24 @@ uint32_t pair_blocks(uint32_t heads, uint32_t seq) { return heads * (((seq + 15)
 
 // Grids that would split keys across blocks run the paired 16-query kernel
 // instead when its rows take vector loads (dim % 4 == 0), the head dim pads
-// to 64 or 128, and it has at least kPairsMinBlocks blocks; smaller grids
-// keep the split launch, which spreads any grid over every CU.
-constexpr uint32_t kPairsMinBlocks = 128;
+// to 64 or 128, and it has at least kPairsMinBlocks blocks, or when each wave
+// has little work: at most kPairsSmallWork key units per wave (a shared unit
+// counts twice, a head-dim-128 unit twice). Other small grids keep the split
+// launch, which spreads any grid over every CU at the cost of a second,
+// merging launch. Measured on MI355X, split against paired (us): H4 S512 D64
+// causal 13.2 / 11.7 and H4 S256 D64 noncausal 11.3 / 10.1 (4 units per
+// wave); H4 S512 D64 noncausal 13.3 / 14.8 (8); H2 S1024 D64 causal 16.4 /
+// 16.5 (8); H2 S1024 D64 noncausal 17.5 / 23.7 and H1 S2048 D64 causal 22.0 /
+// 25.3 (16).
+constexpr uint32_t kPairsMinBlocks = 128, kPairsSmallWork = 6;
 bool use_pairs(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
-    return split_plan(heads, seq, causal).slices > 1 && dim % 4 == 0 && padded_dim(dim) >= 64 &&
-           pair_blocks(heads, seq) >= kPairsMinBlocks;
+    if (split_plan(heads, seq, causal).slices <= 1 || dim % 4 != 0 || padded_dim(dim) < 64) return false;
+    if (pair_blocks(heads, seq) >= kPairsMinBlocks) return true;
+    const int dp = padded_dim(dim);
+    const uint32_t x = (seq + 15) / 16;  // 16-query blocks, and key units
+    const uint32_t cost = causal ? x + 1 : 2 * x;
+    const uint32_t waves = dp == 64 ? pairs::Config<64>::kWaves : pairs::Config<128>::kWaves;
+    return cost * uint32_t(dp / 64) <= kPairsSmallWork * waves;
 }
 
 template <int DP>

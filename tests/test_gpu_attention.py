@@ -165,6 +165,10 @@ def test_split_key_grids(runtime, h, s, d, causal):
     # pipeline), ragged and whole; long rows; head dims 128 and 96.
     (8, 1000, 64, False), (6, 1008, 64, False), (8, 1008, 64, True), (2, 3000, 64, False),
     (8, 1024, 128, False), (5, 1100, 96, False),
+    # Grids below 128 pair blocks whose waves hold little work (the reference's
+    # lab configs H4 S512 causal and H4 S256; tiny and ragged grids).
+    (4, 512, 64, True), (4, 256, 64, False), (4, 256, 64, True), (1, 256, 64, False), (1, 128, 64, True),
+    (1, 100, 64, True), (3, 72, 48, True),
 ])
 def test_paired_small_grids(runtime, h, s, d, causal):
     # Grids that would otherwise split keys across blocks run 16-query waves
