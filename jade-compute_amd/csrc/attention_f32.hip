@@ -634,14 +634,15 @@ __device__ inline void load_unit(const float *__restrict__ K, const float *__res
 }
 }  // namespace pairs
 
-// Grid: heads * ceil(X / 2) blocks, block b = pair b / heads of head b % heads.
+// Grid: heads * ceil(X / 2) blocks, block b = pair b / heads of head b % heads
+// (with `singles`, heads * X blocks, block b = query block b / heads alone).
 // Needs dim % 4 == 0 and 16-byte aligned tensors (vector loads), dim <= DP.
 template <int DP, bool CAUSAL, int CH, int NW>
 __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__restrict__ Q,
                                                                         const float *__restrict__ K,
                                                                         const float *__restrict__ V,
                                                                         float *__restrict__ O, int seq, int dim,
-                                                                        float qscale, int heads) {
+                                                                        float qscale, int heads, int singles) {
     using namespace pairs;
     using KV = UnitKV<DP>;
     constexpr int D4 = DP / 4, NDB = DP / 16;
@@ -656,7 +657,8 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     const int i = lane & 15, g = lane >> 4;
     const int blocks_q = (seq + kUnit - 1) / kUnit;  // query blocks, and key units
     const int head = int(blockIdx.x) % heads, pair = int(blockIdx.x) / heads;
-    const int xa = pair, xb = blocks_q - 1 - pair;  // xa <= xb
+    // `singles`: one query block per workgroup (noncausal small grids).
+    const int xa = pair, xb = singles ? pair : blocks_q - 1 - pair;  // xa <= xb
     const bool single = xa == xb;
     // Key units [0, uc) serve both query blocks, [uc, ub) only xb (xa's keys
     // are a prefix of xb's under the causal mask, and all of them without it).
@@ -1072,42 +1074,69 @@ hipError_t launch_online(hipStream_t stream, const float *q, const float *k, con
 
 
 // Blocks of the paired 16-query launch: heads x ceil(X / 2), X = ceil(seq / 16).
-uint32_t pair_blocks(uint32_t heads, uint32_t seq) { return heads * (((seq + 15) / 16 + 1) / 2); }
+// How a grid that would otherwise split keys across blocks runs the 16-query
+// kernel: not at all, on pairs of query blocks, or on single query blocks.
+enum class PairMode { None, Pairs, Singles };
 
-// Grids that would split keys across blocks run the paired 16-query kernel
-// instead when its rows take vector loads (dim % 4 == 0), the head dim pads
-// to 64 or 128, and it has at least kPairsMinBlocks blocks, or when each wave
-// has little work: at most kPairsSmallWork key units per wave (a shared unit
-// counts twice, a head-dim-128 unit twice). Other small grids keep the split
-// launch, which spreads any grid over every CU at the cost of a second,
-// merging launch. Measured on MI355X, split against paired (us): H4 S512 D64
-// causal 13.2 / 11.7 and H4 S256 D64 noncausal 11.3 / 10.1 (4 units per
-// wave); H4 S512 D64 noncausal 13.3 / 14.8 (8); H2 S1024 D64 causal 16.4 /
+uint32_t query_units(uint32_t seq) { return (seq + 15) / 16; }
+uint32_t pair_blocks(uint32_t heads, uint32_t seq) { return heads * ((query_units(seq) + 1) / 2); }
+
+// Paired blocks run when the rows take vector loads (dim % 4 == 0), the head
+// dim pads to 64 or 128, and the launch has at least kPairsMinBlocks blocks,
+// or each wave has little work: at most kPairsSmallWork key units per wave (a
+// shared unit counts twice, a head-dim-128 unit twice). Other small grids
+// keep the split launch, which spreads any grid over every CU at the cost of a
+// second, merging launch. Measured on MI355X, split against paired (us): H4
+// S512 D64 causal 13.2 / 11.7 and H4 S256 D64 noncausal 11.3 / 10.1 (4 units
+// per wave); H4 S512 D64 noncausal 13.3 / 14.8 (8); H2 S1024 D64 causal 16.4 /
 // 16.5 (8); H2 S1024 D64 noncausal 17.5 / 23.7 and H1 S2048 D64 causal 22.0 /
 // 25.3 (16).
+//
+// Noncausal rows need no pairing for balance: where one query block per
+// workgroup still fits one round of the CUs, it halves each wave's work (at
+// the price of loading each K/V unit for 16 queries instead of 32). Taken
+// with at least kSinglesFullBlocks workgroups and at most kSinglesMaxWork
+// units per wave, or with at most kSinglesSmallWork units per wave. Measured
+// (us), split or paired against singles: H1 S4096 D64 49.7 / 42.6 (256
+// workgroups, 32 units per wave), H2 S2048 D64 30.3 / 24.3, H3 S1024 D64
+// 19.3 / 15.5 (192), H4 S1024 D64 23.8 (paired) / 15.5, H8 S512 D128 26.7 /
+// 20.3, H4 S1024 D128 35.7 / 32.3 (32 units); H2 S1024 D64 17.5 / 15.5 (128
+// workgroups, 8 units); against them H2 S2048 D128 54.5 / 55.8 (64 units) and
+// H1 S2048 D64 22.6 / 24.2 (128 workgroups, 16 units).
 constexpr uint32_t kPairsMinBlocks = 128, kPairsSmallWork = 6;
-bool use_pairs(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
-    if (split_plan(heads, seq, causal).slices <= 1 || dim % 4 != 0 || padded_dim(dim) < 64) return false;
-    if (pair_blocks(heads, seq) >= kPairsMinBlocks) return true;
+constexpr uint32_t kSinglesMaxBlocks = 256, kSinglesFullBlocks = 192, kSinglesMaxWork = 32, kSinglesSmallWork = 8;
+PairMode pair_mode(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+    if (split_plan(heads, seq, causal).slices <= 1 || dim % 4 != 0 || padded_dim(dim) < 64) return PairMode::None;
     const int dp = padded_dim(dim);
-    const uint32_t x = (seq + 15) / 16;  // 16-query blocks, and key units
-    const uint32_t cost = causal ? x + 1 : 2 * x;
+    const uint32_t x = query_units(seq), scale = uint32_t(dp / 64);
     const uint32_t waves = dp == 64 ? pairs::Config<64>::kWaves : pairs::Config<128>::kWaves;
-    return cost * uint32_t(dp / 64) <= kPairsSmallWork * waves;
+    const uint64_t singles = uint64_t(heads) * x;
+    const uint32_t single_work = x * scale;  // per workgroup; per wave after dividing by `waves`
+    if (!causal && singles <= kSinglesMaxBlocks &&
+        ((singles >= kSinglesFullBlocks && single_work <= kSinglesMaxWork * waves) ||
+         single_work <= kSinglesSmallWork * waves))
+        return PairMode::Singles;
+    if (pair_blocks(heads, seq) >= kPairsMinBlocks) return PairMode::Pairs;
+    const uint32_t cost = causal ? x + 1 : 2 * x;
+    return cost * scale <= kPairsSmallWork * waves ? PairMode::Pairs : PairMode::None;
+}
+uint32_t pair_mode_blocks(uint32_t heads, uint32_t seq, PairMode mode) {
+    return mode == PairMode::Singles ? heads * query_units(seq) : pair_blocks(heads, seq);
 }
 
 template <int DP>
 hipError_t launch_pairs(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
-                        uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
+                        uint32_t heads, uint32_t seq, uint32_t dim, bool causal, PairMode mode) {
     using C = pairs::Config<DP>;
     const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
-    const dim3 grid(pair_blocks(heads, seq)), block(C::kWaves * 64);
+    const dim3 grid(pair_mode_blocks(heads, seq, mode)), block(C::kWaves * 64);
+    const int singles = mode == PairMode::Singles ? 1 : 0;
     if (causal)
         hipLaunchKernelGGL((attention_pairs_mfma<DP, true, C::kChunk, C::kWaves>), grid, block, 0, stream, q, k, v,
-                           out, int(seq), int(dim), qscale, int(heads));
+                           out, int(seq), int(dim), qscale, int(heads), singles);
     else
         hipLaunchKernelGGL((attention_pairs_mfma<DP, false, C::kChunk, C::kWaves>), grid, block, 0, stream, q, k, v,
-                           out, int(seq), int(dim), qscale, int(heads));
+                           out, int(seq), int(dim), qscale, int(heads), singles);
     return hipGetLastError();
 }
 
@@ -1115,8 +1144,8 @@ template <int DP>
 hipError_t dispatch_dim(hipStream_t stream, const float *q, const float *k, const float *v, float *out,
                         float *workspace, uint32_t heads, uint32_t seq, uint32_t dim, bool causal, bool vec) {
     if constexpr (DP >= 64) {
-        if (vec && use_pairs(heads, seq, dim, causal))
-            return launch_pairs<DP>(stream, q, k, v, out, heads, seq, dim, causal);
+        const PairMode mode = pair_mode(heads, seq, dim, causal);
+        if (vec && mode != PairMode::None) return launch_pairs<DP>(stream, q, k, v, out, heads, seq, dim, causal, mode);
     }
     const SplitPlan plan = split_plan(heads, seq, causal);
     if (plan.slices > 1) {
@@ -1154,11 +1183,16 @@ uint32_t lds_bytes(int nw) {
 
 LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
     const int dp = padded_dim(dim);
-    if (use_pairs(heads, seq, dim, causal))
-        return {dp == 64 ? "attention_online_mfma16_d64_pairs" : "attention_online_mfma16_d128_pairs",
-                {pair_blocks(heads, seq), 1, 1},
+    const PairMode mode = pair_mode(heads, seq, dim, causal);
+    if (mode != PairMode::None) {
+        static const char *const names[2][2] = {
+            {"attention_online_mfma16_d64_pairs", "attention_online_mfma16_d128_pairs"},
+            {"attention_online_mfma16_d64_singles", "attention_online_mfma16_d128_singles"}};
+        return {names[mode == PairMode::Singles][dp == 64 ? 0 : 1],
+                {pair_mode_blocks(heads, seq, mode), 1, 1},
                 {uint32_t(pairs_waves(dp) * 64), 1, 1},
                 uint32_t(pairs_waves(dp) * 2 * pairs::kUnit * ((dp + 4) * sizeof(float) + sizeof(float2)))};
+    }
     const int nw = waves_for(heads, seq);
     const uint32_t bq = 32u * nw;
     const SplitPlan plan = split_plan(heads, seq, causal);
@@ -1174,7 +1208,7 @@ LaunchShape attention_online_shape(uint32_t heads, uint32_t seq, uint32_t dim, b
 }
 
 size_t attention_online_workspace_bytes(uint32_t heads, uint32_t seq, uint32_t dim, bool causal) {
-    if (use_pairs(heads, seq, dim, causal)) return 0;
+    if (pair_mode(heads, seq, dim, causal) != PairMode::None) return 0;
     const uint32_t splits = split_plan(heads, seq, causal).slices;
     if (splits <= 1) return 0;
     return (split_part_floats(heads, seq, dim, splits) + 2 * size_t(splits) * heads * seq) * sizeof(float);

@@ -175,11 +175,29 @@ def test_paired_small_grids(runtime, h, s, d, causal):
     # that split each block's keys among themselves and merge in LDS: one
     # launch, no workspace.
     kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
-    assert kernel.launch["kernel"].endswith("_pairs") and kernel.description["workspace_bytes"] == 0, kernel.launch
+    assert kernel.launch["kernel"].endswith(("_pairs", "_singles")), kernel.launch
+    assert kernel.description["workspace_bytes"] == 0
     n = h * s * d
     q, k, v = orc.normal(n, 0x4141), orc.normal(n, 0x4242), orc.normal(n, 0x4343)
     got = run_online(runtime, h, s, d, causal, q, k, v, repeats=2)
     want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("h,s,d", [(4, 512, 64), (2, 1024, 64), (4, 1024, 64), (2, 2048, 64), (3, 700, 48),
+                                   (4, 1024, 128), (1, 100, 64), (16, 256, 64), (1, 4096, 64)])
+def test_single_query_block_grids(runtime, h, s, d):
+    # Noncausal grids of at most 256 16-query blocks that fill most of the
+    # chip or hold little work per wave run one query block per workgroup
+    # (every key unit serves that block alone).
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": False})
+    assert kernel.launch["kernel"].endswith("_singles"), kernel.launch
+    assert kernel.launch["grid"][0] == h * ((s + 15) // 16) and kernel.description["workspace_bytes"] == 0
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x5151), orc.normal(n, 0x5252), orc.normal(n, 0x5353)
+    got = run_online(runtime, h, s, d, False, q, k, v, repeats=2)
+    want = orc.attention_reference(h, s, d, False, q, k, v)
     check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
     assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
 
