@@ -338,3 +338,37 @@ def test_noalloc_scratch_covers_every_split_plan():
                     continue
                 most = max(most, describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["workspace_bytes"])
     assert 0 < most <= limit, most
+
+
+@pytest.mark.parametrize("heads,seq,dim,causal,kernel,blocks", [
+    # Grids that fill the chip with 128-query blocks: the flash kernel.
+    (128, 4096, 128, True, "attention_online_mfma_d128", 128),
+    (64, 2048, 128, True, "attention_online_mfma_d128", 64),
+    (32, 2048, 64, True, "attention_online_mfma_d64", 32),
+    (1, 64, 64, True, "attention_online_mfma_d64", 1),
+    # Config C3: pairs of 16-query blocks, 256 workgroups.
+    (8, 1024, 64, True, "attention_online_mfma16_d64_pairs", 256),
+    (8, 1024, 64, False, "attention_online_mfma16_d64_pairs", 256),
+    (2, 2048, 128, False, "attention_online_mfma16_d128_pairs", 128),
+    # Small grids with little work per wave: pairs (causal) or single query
+    # blocks (noncausal, at most 256 workgroups).
+    (4, 512, 64, True, "attention_online_mfma16_d64_pairs", 64),
+    (4, 512, 64, False, "attention_online_mfma16_d64_singles", 128),
+    (4, 256, 64, False, "attention_online_mfma16_d64_singles", 64),
+    (2, 1024, 64, False, "attention_online_mfma16_d64_singles", 128),
+    (4, 1024, 64, False, "attention_online_mfma16_d64_singles", 256),
+    # More work per wave on few workgroups, head dims of at most 32 and
+    # unaligned rows: the split launch and its merge.
+    (2, 1024, 64, True, "attention_online_mfma_d64_split", 144),
+    (1, 2048, 64, False, "attention_online_mfma_d64_split", 256),
+    (1, 2048, 64, True, "attention_online_mfma_d64_split", 136),
+    (2, 1000, 128, False, "attention_online_mfma_d128_split", 256),
+    (3, 200, 5, True, "attention_online_mfma_d32_split", 18),
+    (2, 513, 32, False, "attention_online_mfma_d32_split", 90),
+])
+def test_attention_kernel_selection(heads, seq, dim, causal, kernel, blocks):
+    # The online-attention planner's choice per grid (attention_f32.hip:
+    # pair_mode, split_plan, waves_for); the 16-query kernels need no workspace.
+    d = describe({"op": "attention_online", "heads": heads, "seq": seq, "dim": dim, "causal": causal})
+    assert d["launch"]["kernel"] == kernel and d["launch"]["grid"][0] == blocks, d["launch"]
+    assert (d["workspace_bytes"] > 0) == kernel.endswith("_split")
