@@ -571,6 +571,7 @@ struct Config {
     static constexpr int kWaves = DP == 64 ? 8 : 4, kChunk = 1;
 };
 constexpr int kUnit = 16;  // keys per unit, queries per query block
+constexpr float kLazyMax = 8.0f;  // log2 units a tile may exceed the running reference maximum
 constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
 
 template <int DP>
@@ -785,7 +786,13 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         }
     };
     // Masks are selects on a wave-uniform flag (MASK false: the caller knows
-    // no key of the chunk is masked); the rescale is unconditional.
+    // no key of the chunk is masked). The running maximum is a reference that
+    // moves only when a tile exceeds it by more than kLazyMax (log2 units), so
+    // the weights stay at most 2^kLazyMax and the accumulators rarely need a
+    // rescale: the softmax is exact for any reference, and the results differ
+    // from a tight maximum only by rounding. Returns the factor the
+    // accumulators must take before the next P.V (1 when the reference held);
+    // `rescale` applies it.
     auto update = [&](f32x4(&s)[CH], int t, int x, State &st, auto mask) {
         constexpr bool MASK = decltype(mask)::value;
         const int query = x * kUnit + i;
@@ -805,7 +812,7 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
             }
         }
         tile_max = pairs::lanes_max(tile_max);
-        const float next_max = fmaxf(st.row_max, tile_max);
+        const float next_max = tile_max > st.row_max + kLazyMax ? tile_max : st.row_max;
         const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
         float tile_sum = 0.f;
 #pragma unroll
@@ -817,8 +824,18 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
             }
         st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
         st.row_max = next_max;
+        return old_weight;
+    };
+    // The accumulators' pending rescale, skipped (wave-uniform) when no lane's
+    // reference moved.
+    auto rescale = [&](float wa, float wb) {
+        if (__any(wa != 1.0f || wb != 1.0f)) {
 #pragma unroll
-        for (int b = 0; b < NDB; ++b) st.acc[b] *= old_weight;
+            for (int b = 0; b < NDB; ++b) {
+                sa.acc[b] *= wa;
+                sb.acc[b] *= wb;
+            }
+        }
     };
     auto pv = [&](const KV(&kv)[CH], const f32x4(&s)[CH], State &st) {
 #pragma unroll
@@ -836,8 +853,9 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     auto both_full = [&](const KV(&kv)[CH], int t) {
         f32x4 s_a[CH], s_b[CH];
         scores2(kv, s_a, s_b);
-        update(s_a, t, xa, sa, std::true_type{});
-        update(s_b, t, xb, sb, std::true_type{});
+        const float wa = update(s_a, t, xa, sa, std::true_type{});
+        const float wb = update(s_b, t, xb, sb, std::true_type{});
+        rescale(wa, wb);
         pv(kv, s_a, sa);
         pv(kv, s_b, sb);
     };
@@ -929,8 +947,10 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         };
         // Chunk t's softmax and P.V from its scores (s_a, s_b) and V.
         auto consume = [&](int t, const KV(&vcur)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
-            if constexpr (TWO) update(s_a, t, xa, sa, std::false_type{});
-            update(s_b, t, xb, sb, std::false_type{});
+            float wa = 1.0f;
+            if constexpr (TWO) wa = update(s_a, t, xa, sa, std::false_type{});
+            const float wb = update(s_b, t, xb, sb, std::false_type{});
+            rescale(wa, wb);
             if constexpr (TWO) pv(vcur, s_a, sa);
             pv(vcur, s_b, sb);
         };
@@ -948,14 +968,13 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
                         f32x4(&s_a)[CH], f32x4(&s_b)[CH], f32x4(&n_a)[CH], f32x4(&n_b)[CH]) {
             load_k(kfree, min(t + 2 * CH, last));
             load_v(vnext, min(t + CH, last));
-            if constexpr (TWO) update(s_a, t, xa, sa, std::false_type{});
-            update(s_b, t, xb, sb, std::false_type{});
+            float wa = 1.0f;
+            if constexpr (TWO) wa = update(s_a, t, xa, sa, std::false_type{});
+            const float wb = update(s_b, t, xb, sb, std::false_type{});
             scores(knext, n_a, n_b);
-            if constexpr (TWO) pv(vcur, s_a, sa);
-            pv(vcur, s_b, sb);
-            // CH D4 score MFMAs and 4 CH NDB P.V MFMAs per query block, CH DP/8
-            // vector loads; the softmax fills the MFMA shadow.
-            constexpr int kMfma = (TWO ? 2 : 1) * CH * (D4 + 4 * NDB), kLoads = CH * DP / 8;
+            // CH D4 score MFMAs per query block and CH DP/8 vector loads; the
+            // softmax fills the MFMA shadow.
+            constexpr int kMfma = (TWO ? 2 : 1) * CH * D4, kLoads = CH * DP / 8;
 #pragma unroll
             for (int j = 0; j < kLoads; ++j) {
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one load
@@ -967,6 +986,10 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
+            rescale(wa, wb);
+            if constexpr (TWO) pv(vcur, s_a, sa);
+            pv(vcur, s_b, sb);
             // Nothing crosses into the next step: its scores wait on this
             // step's loads.
             __builtin_amdgcn_sched_barrier(0);
