@@ -41,6 +41,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBKV = 64;  // keys per LDS tile (two 32-key sub-tiles)
+// Online softmax with a lazy reference maximum: the reference moves only when
+// a tile's maximum exceeds it by more than kLazyMax (log2 units), so every
+// weight exp2(s - reference) stays at most 2^kLazyMax and the accumulators
+// take a rescale only when the reference moves.
+constexpr float kLazyMax = 8.0f;
 constexpr uint32_t kMaxSplits = 16;  // key slices per row of a split launch, at most
 constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
 
@@ -254,9 +259,12 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
                     }
                 }
             }
-            // The online max / normaliser update (log2 domain).
+            // The online max / normaliser update (log2 domain). The running
+            // maximum is a lazy reference (kLazyMax): it moves only
+            // when a tile exceeds it by more than 2^8, so the rescale below is
+            // rarely needed.
             tile_max = halves_max(tile_max);
-            float next_max = fmaxf(row_max, tile_max);
+            float next_max = tile_max > row_max + kLazyMax ? tile_max : row_max;
             // A slice that starts past key 0 can meet a query with no live key
             // yet; keep its max finite so the weights below are 0, not NaN.
             if (SPLIT && next_max == -INFINITY) next_max = 0.f;
@@ -571,7 +579,6 @@ struct Config {
     static constexpr int kWaves = DP == 64 ? 8 : 4, kChunk = 1;
 };
 constexpr int kUnit = 16;  // keys per unit, queries per query block
-constexpr float kLazyMax = 8.0f;  // log2 units a tile may exceed the running reference maximum
 constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
 
 template <int DP>
