@@ -708,6 +708,10 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     load_q(xa, qa);
     load_q(xb, qb);
 
+    // Per query block: O^T accumulators, the query's reference maximum (equal
+    // in its four lanes) and this lane's share of the normaliser (the sum
+    // over the query's keys 16u + 4g + r held by lane 16g + i); the four
+    // shares are added once, when the rows are merged.
     struct State {
         f32x4 acc[NDB];
         float row_max, row_sum;
@@ -760,7 +764,7 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
                     tile_sum += s[c][r];
                 }
             }
-        st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
+        st.row_sum = st.row_sum * old_weight + tile_sum;
         st.row_max = next_max;
         if (__any(old_weight != 1.0f)) {
 #pragma unroll
@@ -792,57 +796,65 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
             }
         }
     };
-    // Masks are selects on a wave-uniform flag (MASK false: the caller knows
-    // no key of the chunk is masked). The running maximum is a reference that
-    // moves only when a tile exceeds it by more than kLazyMax (log2 units), so
-    // the weights stay at most 2^kLazyMax and the accumulators rarely need a
-    // rescale: the softmax is exact for any reference, and the results differ
-    // from a tight maximum only by rounding. Returns the factor the
-    // accumulators must take before the next P.V (1 when the reference held);
-    // `rescale` applies it.
-    auto update = [&](f32x4(&s)[CH], int t, int x, State &st, auto mask) {
-        constexpr bool MASK = decltype(mask)::value;
-        const int query = x * kUnit + i;
-        float tile_max = -INFINITY;
+    // The online softmax of one chunk for both query blocks (TWO) or xb
+    // alone, in place on the scores. Masks are selects on a wave-uniform flag
+    // (MASK false: the caller knows no key of the chunk is masked). The
+    // reference maximum is lazy (kLazyMax): a wave vote asks whether any
+    // lane's own scores exceed its query's reference by more than kLazyMax;
+    // only then (the first chunk, and rare jumps) do the queries take their
+    // exact maxima across their four lanes, and the normaliser shares and
+    // accumulators their rescale. Otherwise no cross-lane work is needed: the
+    // weights exp2(s - reference) stay at most 2^kLazyMax. Softmax is exact
+    // for any reference, so this differs from a tight maximum by rounding only.
+    auto softmax2 = [&](f32x4(&s_a)[CH], f32x4(&s_b)[CH], int t, auto two, auto mask) {
+        constexpr bool TWO = decltype(two)::value, MASK = decltype(mask)::value;
+        auto lane_max = [&](f32x4(&s)[CH], int x) {
+            const int query = x * kUnit + i;
+            float m = -INFINITY;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-            const int key0 = (t + c) * kUnit;
-            const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
+            for (int c = 0; c < CH; ++c) {
+                const int key0 = (t + c) * kUnit;
+                const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (MASK) {
-                    const int key = key0 + 4 * g + r;
-                    const bool live = key < seq && (!CAUSAL || key <= query);
-                    s[c][r] = (masked_unit && !live) ? -INFINITY : s[c][r];
+                for (int r = 0; r < 4; ++r) {
+                    if (MASK) {
+                        const int key = key0 + 4 * g + r;
+                        const bool live = key < seq && (!CAUSAL || key <= query);
+                        s[c][r] = (masked_unit && !live) ? -INFINITY : s[c][r];
+                    }
+                    m = fmaxf(m, s[c][r]);
                 }
-                tile_max = fmaxf(tile_max, s[c][r]);
             }
+            return m;
+        };
+        const float ma = TWO ? lane_max(s_a, xa) : -INFINITY, mb = lane_max(s_b, xb);
+        if (__any(ma > sa.row_max + kLazyMax || mb > sb.row_max + kLazyMax)) {
+            // Every query of a processed chunk has a live key, so the new
+            // maxima are finite. Exact maxima: weights at most 1 for this chunk.
+            auto move = [&](float m, State &st) {
+                const float next = fmaxf(st.row_max, pairs::lanes_max(m));
+                const float w = __builtin_amdgcn_exp2f(st.row_max - next);
+                st.row_max = next;
+                st.row_sum *= w;
+#pragma unroll
+                for (int b = 0; b < NDB; ++b) st.acc[b] *= w;
+            };
+            if constexpr (TWO) move(ma, sa);
+            move(mb, sb);
         }
-        tile_max = pairs::lanes_max(tile_max);
-        const float next_max = tile_max > st.row_max + kLazyMax ? tile_max : st.row_max;
-        const float old_weight = __builtin_amdgcn_exp2f(st.row_max - next_max);
-        float tile_sum = 0.f;
+        auto weigh = [&](f32x4(&s)[CH], State &st) {
+            float sum = 0.f;
 #pragma unroll
-        for (int c = 0; c < CH; ++c)
+            for (int c = 0; c < CH; ++c)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - next_max);
-                tile_sum += s[c][r];
-            }
-        st.row_sum = st.row_sum * old_weight + pairs::lanes_sum(tile_sum);
-        st.row_max = next_max;
-        return old_weight;
-    };
-    // The accumulators' pending rescale, skipped (wave-uniform) when no lane's
-    // reference moved.
-    auto rescale = [&](float wa, float wb) {
-        if (__any(wa != 1.0f || wb != 1.0f)) {
-#pragma unroll
-            for (int b = 0; b < NDB; ++b) {
-                sa.acc[b] *= wa;
-                sb.acc[b] *= wb;
-            }
-        }
+                for (int r = 0; r < 4; ++r) {
+                    s[c][r] = __builtin_amdgcn_exp2f(s[c][r] - st.row_max);
+                    sum += s[c][r];
+                }
+            st.row_sum += sum;
+        };
+        if constexpr (TWO) weigh(s_a, sa);
+        weigh(s_b, sb);
     };
     auto pv = [&](const KV(&kv)[CH], const f32x4(&s)[CH], State &st) {
 #pragma unroll
@@ -860,9 +872,7 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     auto both_full = [&](const KV(&kv)[CH], int t) {
         f32x4 s_a[CH], s_b[CH];
         scores2(kv, s_a, s_b);
-        const float wa = update(s_a, t, xa, sa, std::true_type{});
-        const float wb = update(s_b, t, xb, sb, std::true_type{});
-        rescale(wa, wb);
+        softmax2(s_a, s_b, t, std::true_type{}, std::true_type{});
         pv(kv, s_a, sa);
         pv(kv, s_b, sb);
     };
@@ -954,10 +964,7 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         };
         // Chunk t's softmax and P.V from its scores (s_a, s_b) and V.
         auto consume = [&](int t, const KV(&vcur)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
-            float wa = 1.0f;
-            if constexpr (TWO) wa = update(s_a, t, xa, sa, std::false_type{});
-            const float wb = update(s_b, t, xb, sb, std::false_type{});
-            rescale(wa, wb);
+            softmax2(s_a, s_b, t, two, std::false_type{});
             if constexpr (TWO) pv(vcur, s_a, sa);
             pv(vcur, s_b, sb);
         };
@@ -973,11 +980,12 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         // run re-read its last chunk and are never used.
         auto step = [&](int t, KV(&kfree)[CH], const KV(&knext)[CH], const KV(&vcur)[CH], KV(&vnext)[CH],
                         f32x4(&s_a)[CH], f32x4(&s_b)[CH], f32x4(&n_a)[CH], f32x4(&n_b)[CH]) {
+            // The softmax's rare rescale branch comes first, so that its
+            // exponentials, the loads and the next chunk's score MFMAs share
+            // one basic block.
+            softmax2(s_a, s_b, t, two, std::false_type{});
             load_k(kfree, min(t + 2 * CH, last));
             load_v(vnext, min(t + CH, last));
-            float wa = 1.0f;
-            if constexpr (TWO) wa = update(s_a, t, xa, sa, std::false_type{});
-            const float wb = update(s_b, t, xb, sb, std::false_type{});
             scores(knext, n_a, n_b);
             // CH D4 score MFMAs per query block and CH DP/8 vector loads; the
             // softmax fills the MFMA shadow.
@@ -994,7 +1002,6 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
-            rescale(wa, wb);
             if constexpr (TWO) pv(vcur, s_a, sa);
             pv(vcur, s_b, sb);
             // Nothing crosses into the next step: its scores wait on this
@@ -1055,7 +1062,8 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
                 const f32x4 o = {st.acc[4 * e][r], st.acc[4 * e + 1][r], st.acc[4 * e + 2][r], st.acc[4 * e + 3][r]};
                 part[slot][i][(D4 * g + NDB * r) / 4 + e] = o;
             }
-        if (g == 0) mls[slot][i] = make_float2(st.row_max, st.row_sum);
+        const float row_sum = pairs::lanes_sum(st.row_sum);  // the query's four shares
+        if (g == 0) mls[slot][i] = make_float2(st.row_max, row_sum);
     };
     flush(sa, wave * 2);
     flush(sb, wave * 2 + 1);
