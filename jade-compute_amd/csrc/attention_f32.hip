@@ -814,16 +814,17 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
                 const int key0 = (t + c) * kUnit;
-                const bool masked_unit = (CAUSAL && t + c == x) || key0 + kUnit > seq;  // wave-uniform
+                // Only a unit on the causal diagonal or past the end of seq
+                // holds masked keys (wave-uniform, rare).
+                if (MASK && ((CAUSAL && t + c == x) || key0 + kUnit > seq)) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    if (MASK) {
+                    for (int r = 0; r < 4; ++r) {
                         const int key = key0 + 4 * g + r;
-                        const bool live = key < seq && (!CAUSAL || key <= query);
-                        s[c][r] = (masked_unit && !live) ? -INFINITY : s[c][r];
+                        if (!(key < seq && (!CAUSAL || key <= query))) s[c][r] = -INFINITY;
                     }
-                    m = fmaxf(m, s[c][r]);
                 }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) m = fmaxf(m, s[c][r]);
             }
             return m;
         };
@@ -886,25 +887,29 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         attend(kv, t, n, xb, qb, sb);
     };
 
-    // Runs of whole chunks with no masked key take a software pipeline:
-    // chunk c's scores are computed in step c-1, so in step c the MFMAs of
-    // chunk c+1's scores sit beside chunk c's softmax, then chunk c's P.V
-    // follows. K runs two chunks ahead of use, V one; each has two buffers.
-    // The step is one basic block whose MFMAs and VALU work are interleaved
-    // explicitly. Two runs qualify: shared units below xa's diagonal unit
-    // (both query blocks), and xb-only units below xb's diagonal unit (xb
-    // alone); both also end at the last whole unit of seq. What is left of
-    // [u0, u1) takes the chunk loop further down.
+    // A wave's units run as a software pipeline of whole chunks: chunk c's
+    // scores are computed in step c-1, so in step c the MFMAs of chunk c+1's
+    // scores sit beside chunk c's softmax, then chunk c's P.V follows. K runs
+    // two chunks ahead of use, V one; each has two buffers. The step's
+    // exponentials, loads and score MFMAs share one basic block with an
+    // explicit interleave; a unit holding masked keys (a diagonal unit, the
+    // ragged last unit) takes its masks behind a wave-uniform branch. Two runs:
+    // the shared units [u0, uc) (both query blocks) and the xb-only units
+    // [uc, u1) (xb alone). What a run leaves over (less than a chunk) takes
+    // the chunk loop further down.
     // The pipeline's loads are buffer loads: a per-lane byte offset fixed for
     // the kernel plus the unit's row offset as a scalar, so a load costs no
-    // address arithmetic (a head's K and V must fit 2 GiB each).
+    // address arithmetic (a head's K and V must fit 2 GiB each); rows past
+    // seq read zero.
     const bool offsets_fit = size_t(seq) * size_t(dim) * 4u < (size_t(1) << 31);
-    auto steps_in = [&](int lo, int hi) { return offsets_fit && hi - lo >= 2 * CH ? (hi - lo) / CH : 0; };
-    const int whole = seq / kUnit;
-    const int n_two = steps_in(u0, min(u1, single ? 0 : (CAUSAL ? xa : whole)));  // wave-uniform
+    auto steps_in = [&](int lo, int hi) { return offsets_fit && hi - lo >= CH ? (hi - lo) / CH : 0; };
+    // Noncausal runs stop at the last whole unit (their only masked unit is
+    // the ragged last one), so their steps compile without the mask branch.
+    const int end = CAUSAL ? u1 : min(u1, seq / kUnit);
+    const int n_two = steps_in(u0, min(end, uc));  // wave-uniform
     const int up = u0 + n_two * CH;
     const int b_lo = max(u0, uc);
-    const int n_one = steps_in(b_lo, min(u1, CAUSAL ? xb : whole));  // wave-uniform
+    const int n_one = steps_in(b_lo, min(end, ub));  // wave-uniform
     const int bp = b_lo + n_one * CH;
 
     const uint32_t head_bytes = uint32_t(seq) * uint32_t(dim) * 4u, unit_bytes = kUnit * uint32_t(dim) * 4u;
@@ -964,14 +969,14 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
         };
         // Chunk t's softmax and P.V from its scores (s_a, s_b) and V.
         auto consume = [&](int t, const KV(&vcur)[CH], f32x4(&s_a)[CH], f32x4(&s_b)[CH]) {
-            softmax2(s_a, s_b, t, two, std::false_type{});
+            softmax2(s_a, s_b, t, two, std::bool_constant<CAUSAL>{});
             if constexpr (TWO) pv(vcur, s_a, sa);
             pv(vcur, s_b, sb);
         };
         KV kb0[CH], kb1[CH], vb0[CH], vb1[CH];
         f32x4 sa0[CH], sb0[CH], sa1[CH], sb1[CH];
         load_k(kb0, p0);
-        load_k(kb1, p0 + CH);
+        load_k(kb1, min(p0 + CH, last));
         load_v(vb0, p0);
         scores(kb0, sa0, sb0);
         // Step for chunk t, not the last: scores in (s_a, s_b), V in vcur; the
@@ -983,7 +988,7 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
             // The softmax's rare rescale branch comes first, so that its
             // exponentials, the loads and the next chunk's score MFMAs share
             // one basic block.
-            softmax2(s_a, s_b, t, two, std::false_type{});
+            softmax2(s_a, s_b, t, two, std::bool_constant<CAUSAL>{});
             load_k(kfree, min(t + 2 * CH, last));
             load_v(vnext, min(t + CH, last));
             scores(knext, n_a, n_b);
