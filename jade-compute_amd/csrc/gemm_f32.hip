@@ -1010,8 +1010,9 @@ __global__ __launch_bounds__(big::kThreads) void gemm_f32_mfma_256(const float *
 // product that are never stored; k >= K is zeroed in both operands when the
 // last, partial slice is consumed. At the end waves 1..G-1 leave their sums in
 // LDS and wave 0 adds them in wave order: the result is deterministic. Per
-// element: each slice is a 16-step MFMA chain from zero, added to the wave's
-// running sum.
+// element: a wave's slices form one MFMA chain when the wave has at most six
+// of them; longer K ranges sum each slice as a 16-step chain from zero and add
+// it to the wave's running sum.
 namespace direct {
 constexpr int kDepth = 3;  // slices in flight per wave
 
@@ -1064,21 +1065,27 @@ __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_r
 }
 
 // `valid` = K - (k0 + 16h): operand pairs at s >= valid lie past K. ZB: B is
-// already zero there (buffer loads), so only A is masked.
-template <bool ZB>
+// already zero there (buffer loads), so only A is masked. CHAIN: the slice's
+// MFMAs accumulate straight into the wave's running sum (for waves of at most
+// kChainSlices slices, 192 k); otherwise each slice is summed from zero and
+// folded into the running sum with VALU adds, which bounds the length of the
+// matrix cores' accumulation chains for long K ranges.
+constexpr int kChainSlices = 6;
+template <bool ZB, bool CHAIN>
 __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
     f32x16 part;
 #pragma unroll
     for (int v = 0; v < 16; ++v) part[v] = 0.f;
+    f32x16 &sum = CHAIN ? acc : part;
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
             const float a = i < valid ? s.a[q][e] : 0.f, b = ZB || i < valid ? s.b[i] : 0.f;
-            part = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, part, 0, 0, 0);
+            sum = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, sum, 0, 0, 0);
         }
-    acc += part;
+    if (!CHAIN) acc += part;
 }
 }  // namespace direct
 
@@ -1088,7 +1095,7 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 // BUFA: A is read through buffer loads, which needs ((M-1)*lda + K)*4 < 2^31
 // (per product of a batch); unaligned rows (K % 4 != 0) require it. BUFB: B
 // is read through buffer loads (K*N*4 < 2^31; per product of a batch).
-template <int G, bool BUFA, bool BUFB>
+template <int G, bool BUFA, bool BUFB, bool CHAIN>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
                                                           float *__restrict__ C, int M, int N, int K, int lda,
                                                           int tiles_m, int tiles_n, size_t sa, size_t sb,
@@ -1133,7 +1140,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         for (; i + D <= count; i += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                mma_slice<BUFB>(buf[d], valid(i + d), acc);
+                mma_slice<BUFB, CHAIN>(buf[d], valid(i + d), acc);
                 load_slice<BUFA, BUFB>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(i + d + D), i + d + D < count,
                                        h, buf[d]);
                 // Keep the slices in order: interleaving their independent
@@ -1143,7 +1150,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         }
 #pragma unroll
         for (int d = 0; d < D; ++d)
-            if (i + d < count) mma_slice<BUFB>(buf[d], valid(i + d), acc);
+            if (i + d < count) mma_slice<BUFB, CHAIN>(buf[d], valid(i + d), acc);
     }
     if (G > 1) {
         if (g > 0) {
@@ -1167,19 +1174,29 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
 // One direct launch of G waves per 32x32 tile; A and B through buffer loads
 // when a product's operand is below 2 GiB (A always when `bufa`: unaligned
 // rows, whose limit the caller checks).
-template <int G>
-void launch_direct_g(hipStream_t stream, dim3 grid, bool bufa, const float *a, const float *b, float *c, int m,
-                     int n, int k, int lda, int tiles_m, int tiles_n, size_t sa, size_t sb, size_t sc) {
-    const bool bufb = uint64_t(k) * uint64_t(n) * 4u < (uint64_t(1) << 31);
-    bufa = bufa || (uint64_t(m - 1) * uint64_t(lda) + uint64_t(k)) * 4u < (uint64_t(1) << 31);
+template <int G, bool CHAIN>
+void launch_direct_gc(hipStream_t stream, dim3 grid, bool bufa, bool bufb, const float *a, const float *b, float *c,
+                      int m, int n, int k, int lda, int tiles_m, int tiles_n, size_t sa, size_t sb, size_t sc) {
     const dim3 block(64 * G);
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
     };
     if (bufa)
-        bufb ? go(gemm_f32_direct<G, true, true>) : go(gemm_f32_direct<G, true, false>);
+        bufb ? go(gemm_f32_direct<G, true, true, CHAIN>) : go(gemm_f32_direct<G, true, false, CHAIN>);
     else
-        bufb ? go(gemm_f32_direct<G, false, true>) : go(gemm_f32_direct<G, false, false>);
+        bufb ? go(gemm_f32_direct<G, false, true, CHAIN>) : go(gemm_f32_direct<G, false, false, CHAIN>);
+}
+template <int G>
+void launch_direct_g(hipStream_t stream, dim3 grid, bool bufa, const float *a, const float *b, float *c, int m,
+                     int n, int k, int lda, int tiles_m, int tiles_n, size_t sa, size_t sb, size_t sc) {
+    const bool bufb = uint64_t(k) * uint64_t(n) * 4u < (uint64_t(1) << 31);
+    bufa = bufa || (uint64_t(m - 1) * uint64_t(lda) + uint64_t(k)) * 4u < (uint64_t(1) << 31);
+    // A wave sums the slices g, g + G, ...: at most ceil(slices / G).
+    const bool chain = (k + kBK - 1) / kBK <= direct::kChainSlices * G;
+    if (chain)
+        launch_direct_gc<G, true>(stream, grid, bufa, bufb, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
+    else
+        launch_direct_gc<G, false>(stream, grid, bufa, bufb, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
 }
 
 hipError_t launch_direct(hipStream_t stream, dim3 grid, int g, bool bufa, const float *a, const float *b, float *c,
