@@ -775,78 +775,92 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
 // up waves store U and pass it to the gate waves through LDS; the gate waves
 // store G and Act. Interior tiles only: M % 128 == 0, N % 64 == 0,
 // K % 32 == 0, 16-byte aligned rows.
+//
+// A grid whose last round of 128x64 tiles would leave CUs idle can hand that
+// round's tiles, as whole tile columns at the right edge, to 64x64 tiles
+// (twice as many, half the work each, so every CU takes one): the 128x64
+// tiles cover columns [0, 64 body_tn), the 64x64 tiles the rest, launched
+// after them. A 64x64 tile runs the 64x64 kernel's schedule, which per output
+// is the 128x64 one (the same MFMA chain over k, the same fold every two
+// stages), so the bits do not depend on which tile an output falls in.
 namespace dual {
 using T = Tile<2, 1>;
 constexpr int kWaves = 8, kThreads = 64 * kWaves;
-constexpr int kStage = T::kAStageS + 2 * T::kBStageS;  // A, then B for G, then B for U
-constexpr int kAInst = T::kAStageS * 4 / 1024 / kWaves, kBInst = T::kBStageS * 4 / 1024 / (kWaves / 2);
-static_assert(kAInst * kWaves * 1024 == T::kAStageS * 4 && kBInst * (kWaves / 2) * 1024 == T::kBStageS * 4,
-              "stage loads must split evenly over the waves");
+template <int TM>
+struct Shape {
+    using Tl = Tile<TM, 1>;
+    static constexpr int kStage = Tl::kAStageS + 2 * Tl::kBStageS;  // A, then B for G, then B for U
+    static constexpr int kAInst = Tl::kAStageS * 4 / 1024 / kWaves, kBInst = Tl::kBStageS * 4 / 1024 / (kWaves / 2);
+    static_assert(kAInst * kWaves * 1024 == Tl::kAStageS * 4 && kBInst * (kWaves / 2) * 1024 == Tl::kBStageS * 4,
+                  "stage loads must split evenly over the waves");
+};
+constexpr int kStage = Shape<2>::kStage;  // the LDS stage of either tile fits this one
 
 // Waves 0-3 load B for G, waves 4-7 B for U; all eight load A.
+template <int TM>
 __device__ inline void issue_stage(const float *__restrict__ A, const float *__restrict__ B, int N, int K, int m0,
                                    int n0, int k0, uint32_t stage_lds, int wave, int lane) {
+    using S = Shape<TM>;
     const float *abase = A + size_t(m0) * K + k0;
 #pragma unroll
-    for (int i = 0; i < kAInst; ++i) {  // eight 128-byte A rows per 1 KiB load
-        const int inst = wave * kAInst + i;
+    for (int i = 0; i < S::kAInst; ++i) {  // eight 128-byte A rows per 1 KiB load
+        const int inst = wave * S::kAInst + i;
         const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
         lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
     }
     const float *bbase = B + size_t(k0) * N + n0;
-    const uint32_t sb = stage_lds + (T::kAStageS + (wave >> 2) * T::kBStageS) * 4;
-    constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
+    const uint32_t sb = stage_lds + (S::Tl::kAStageS + (wave >> 2) * S::Tl::kBStageS) * 4;
+    constexpr int kChunks = S::Tl::kBN / 4, kRowsPer = 64 / kChunks;
 #pragma unroll
-    for (int i = 0; i < kBInst; ++i) {  // four 256-byte B rows per 1 KiB load
-        const int inst = (wave & 3) * kBInst + i;
+    for (int i = 0; i < S::kBInst; ++i) {  // four 256-byte B rows per 1 KiB load
+        const int inst = (wave & 3) * S::kBInst + i;
         const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
         lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
     }
 }
-}  // namespace dual
 
-__global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
-    const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu, float *__restrict__ G,
-    float *__restrict__ U, float *__restrict__ Act, int N, int K, int tiles_m, int tiles_n) {
-    using namespace dual;
-    __shared__ float smem[2 * kStage];
-    int tm, tn;
-    tile_coords(tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * T::kBM, n0 = tn * T::kBN;
+// One (64 TM) x 64 tile at (m0, n0): its gate product in waves 0-3, its up
+// product in waves 4-7.
+template <int TM>
+__device__ inline void tile(const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu,
+                            float *__restrict__ G, float *__restrict__ U, float *__restrict__ Act, int N, int K,
+                            int m0, int n0, float *smem) {
+    using S = Shape<TM>;
+    using Tl = typename S::Tl;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
     const int group = wave >> 2, wl = wave & 3;  // group 0: G, group 1: U
     const int wm = wl >> 1, wn = wl & 1;
     const float *B = group ? Bu : Bg;
     const uint32_t lds0 = lds_address(smem);
-    f32x16 acc[2][1];
+    f32x16 acc[TM][1];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][0][v] = 0.f;
     const int nk = K / kBK;
-    dual::issue_stage(A, B, N, K, m0, n0, 0, lds0, wave, lane);
+    issue_stage<TM>(A, B, N, K, m0, n0, 0, lds0, wave, lane);
     drain_vmem();
     __syncthreads();
-    // The 128x64 kernel's schedule: partial sums over two stages, then a fold.
-    f32x16 part[2][1];
+    // The LDS-direct loop's schedule: partial sums over two stages, then a fold.
+    f32x16 part[TM][1];
     for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int k = kt + u;
             if (k < nk) {
-                const float *cur = smem + u * kStage;
+                const float *cur = smem + u * S::kStage;
                 if (k + 1 < nk)
-                    dual::issue_stage(A, B, N, K, m0, n0, (k + 1) * kBK, lds0 + uint32_t((1 - u) * kStage * 4), wave,
-                                      lane);
+                    issue_stage<TM>(A, B, N, K, m0, n0, (k + 1) * kBK, lds0 + uint32_t((1 - u) * S::kStage * 4), wave,
+                                    lane);
                 __builtin_amdgcn_s_setprio(1);
                 if (u == 0)
-                    mma_stage_swz<2, 1, true>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+                    mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
                 else
-                    mma_stage_swz<2, 1, false>(cur, cur + T::kAStageS + group * T::kBStageS, wm, wn, lane, part);
+                    mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
                 if (u == 1 || k + 1 == nk) {
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) acc[i][0] += part[i][0];
+                    for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
                 }
                 __builtin_amdgcn_s_setprio(0);
                 drain_vmem();
@@ -860,10 +874,10 @@ __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
     float *ushare = smem;  // [i][v][256 threads of the U group]
     if (group == 1) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                 U[size_t(row) * N + col] = acc[i][0][v];
                 ushare[(i * 16 + v) * 256 + wl * 64 + lane] = acc[i][0][v];
             }
@@ -871,14 +885,34 @@ __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
     __syncthreads();
     if (group == 1) return;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-            const int row = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
             const float g = acc[i][0][v], u = ushare[(i * 16 + v) * 256 + wl * 64 + lane];
             G[size_t(row) * N + col] = g;
             Act[size_t(row) * N + col] = swiglu(g, u);
         }
+}
+}  // namespace dual
+
+// Workgroups [0, tiles_m body_tn) take the 128x64 tiles of columns
+// [0, 64 body_tn) in the XCD-grouped order; the rest take the 64x64 tiles of
+// the columns right of them, row-major.
+__global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
+    const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu, float *__restrict__ G,
+    float *__restrict__ U, float *__restrict__ Act, int N, int K, int tiles_m, int tiles_n, int body_tn) {
+    __shared__ float smem[2 * dual::kStage];
+    const int body = tiles_m * body_tn;
+    if (int(blockIdx.x) < body) {  // block-uniform
+        const int pos = xcd_order(int(blockIdx.x), body);
+        int tm, tn;
+        grouped_tile(pos, tiles_m, body_tn, tm, tn);
+        dual::tile<2>(A, Bg, Bu, G, U, Act, N, K, tm * 128, tn * 64, smem);
+    } else {
+        const int pos = int(blockIdx.x) - body, edge_n = tiles_n - body_tn;
+        dual::tile<1>(A, Bg, Bu, G, U, Act, N, K, (pos / edge_n) * 64, (body_tn + pos % edge_n) * 64, smem);
+    }
 }
 
 // ---- 256x256 tile, eight waves of 128x64 ---------------------------------
@@ -1670,13 +1704,28 @@ bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
            k % kBK == 0 && dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
 }
 
+// Tile columns at the right edge that the fused launch runs as 64x64 tiles:
+// when a grid of more than one round of 128x64 tiles ends in a partial round
+// of at most half the CUs' worth of tiles that fills whole tile columns, those
+// columns' tiles run as twice as many 64x64 tiles, so the busiest CU holds
+// floor(tiles / CUs) + 1/2 tiles of work instead of floor(tiles / CUs) + 1.
+// The MLP's 4096x2816 outputs: 1408 tiles, 128 past five rounds, four
+// columns of 32 tiles.
+int dual_edge_columns(int tiles_m, int tiles_n) {
+    const int tiles = tiles_m * tiles_n, rem = tiles % kCUs;
+    if (tiles <= kCUs || rem == 0 || rem > kCUs / 2 || rem % tiles_m != 0) return 0;
+    return rem / tiles_m;
+}
+
 hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float *bg, const float *bu, float *g,
                                 float *u, float *act, uint32_t m, uint32_t n, uint32_t k) {
     if (!gemm_f32_dual_swiglu_fits(m, n, k) || !aligned16(a) || !aligned16(bg) || !aligned16(bu))
         return hipErrorInvalidValue;
     const int tiles_m = int(m / dual::T::kBM), tiles_n = int(n / dual::T::kBN);
-    hipLaunchKernelGGL(gemm_f32_dual_swiglu, dim3(unsigned(tiles_m * tiles_n)), dim3(dual::kThreads), 0, stream, a, bg,
-                       bu, g, u, act, int(n), int(k), tiles_m, tiles_n);
+    const int edge_n = dual_edge_columns(tiles_m, tiles_n), body_tn = tiles_n - edge_n;
+    const unsigned grid = unsigned(tiles_m * body_tn + 2 * tiles_m * edge_n);
+    hipLaunchKernelGGL(gemm_f32_dual_swiglu, dim3(grid), dim3(dual::kThreads), 0, stream, a, bg, bu, g, u, act,
+                       int(n), int(k), tiles_m, tiles_n, body_tn);
     return hipGetLastError();
 }
 

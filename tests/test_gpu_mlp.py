@@ -79,11 +79,14 @@ def _run_jobs(runtime, specs, arrays, plan, repeats=1, one_at_a_time=False):
     return out
 
 
-def test_fused_gate_up_swiglu_is_bit_identical(runtime):
+@pytest.mark.parametrize("m,n,k", [
+    (2048, 2048, 256),  # two whole rounds of 128x64 tiles
+    (4096, 2816, 96),   # 1408 tiles: the last four tile columns run as 64x64 tiles; three stages (odd fold)
+])
+def test_fused_gate_up_swiglu_is_bit_identical(runtime, m, n, k):
     # gemm(x, Wg -> G), gemm(x, Wu -> U), swi_glu(G, U -> D) on whole 128x64
     # tiles run as one fused launch; each of G, U and D must equal the three
     # jobs launched one at a time, bit for bit.
-    m, n, k = 2048, 2048, 256
     specs = {"gemm": {"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}, "swiglu": {"op": "swi_glu", "len": m * n}}
     assert "128x64" in runtime.compile(specs["gemm"]).launch["kernel"]
     arrays = {"x": orc.normal(m * k, 0x21), "wg": orc.normal(k * n, 0x22, 0.0, 0.1),

@@ -3,7 +3,9 @@
 shape (x[4096x1024], Wg/Wu [1024x2816]) and at the other shapes the fusion
 rule admits: every global address the kernel reads or writes, every LDS byte
 its LDS-direct loads write, every LDS float its MFMA operand reads and the
-U hand-off touch, lies inside its buffer. The kernel's index formulas are
+U hand-off touch, lies inside its buffer, for both of its tiles (128x64, and
+64x64 for the edge columns of a partial last round). The workgroup-to-tile
+map covers every output exactly once. The kernel's index formulas are
 restated with numpy over all lanes, waves, instructions and stages, so a
 launch that the fusion rule accepts cannot address memory outside the
 bindings or the 64 KiB of LDS it declares."""
@@ -11,13 +13,17 @@ import numpy as np
 import pytest
 
 BK = 32                    # K per stage
-BM, BN = 128, 64           # the gate and up tiles (Tile<2, 1>)
-A_STAGE, B_STAGE = BM * BK, BK * BN   # floats per stage, unpadded
-STAGE = A_STAGE + 2 * B_STAGE         # A, then B for the gate, then B for the up product
-LDS_FLOATS = 2 * STAGE                # two stages: 64 KiB
+BN = 64                    # both tiles are 64 columns wide
 WAVES, LANES = 8, 64
-A_INST = A_STAGE * 4 // 1024 // WAVES          # 1 KiB LDS-direct loads per wave per stage
-B_INST = B_STAGE * 4 // 1024 // (WAVES // 2)
+CUS, GROUP_M = 256, 8
+LDS_FLOATS = 2 * (128 * BK + 2 * BK * BN)   # two stages of the 128x64 tile: 64 KiB
+
+
+def shape(tm):
+    """Per-stage sizes of the (64 tm) x 64 tile (dual::Shape<TM>)."""
+    bm = 64 * tm
+    a_stage, b_stage = bm * BK, BK * BN
+    return bm, a_stage, b_stage, a_stage + 2 * b_stage
 
 
 def swz_a(row):
@@ -28,53 +34,121 @@ def swz_b(row):
     return row & 7
 
 
-def stage_loads():
+def stage_loads(tm):
     """(wave, lane, inst) -> global element offsets relative to the A and B
     stage bases, and LDS byte offsets relative to the stage base
-    (dual::issue_stage)."""
+    (dual::issue_stage<TM>)."""
+    bm, a_stage, b_stage, _ = shape(tm)
+    a_inst = a_stage * 4 // 1024 // WAVES
+    b_inst = b_stage * 4 // 1024 // (WAVES // 2)
+    assert a_inst * WAVES * 1024 == a_stage * 4 and b_inst * (WAVES // 2) * 1024 == b_stage * 4
     wave = np.arange(WAVES)[:, None, None]
     lane = np.arange(LANES)[None, :, None]
-    i = np.arange(A_INST)[None, None, :]
-    inst = wave * A_INST + i
+    i = np.arange(a_inst)[None, None, :]
+    inst = wave * a_inst + i
     row = inst * 8 + (lane >> 3)
     j = (lane & 7) ^ swz_a(row)
     a_rows, a_cols = row, 4 * j                       # A[m0 + row][k0 + 4j .. +3]
     a_lds = inst * 1024 + lane * 16                   # 16 bytes per lane
     chunks = BN // 4
     rows_per = 64 // chunks
-    i = np.arange(B_INST)[None, None, :]
-    inst_b = (wave & 3) * B_INST + i
+    i = np.arange(b_inst)[None, None, :]
+    inst_b = (wave & 3) * b_inst + i
     row_b = inst_b * rows_per + lane // chunks
     j_b = (lane % chunks) ^ swz_b(row_b)
     b_rows, b_cols = row_b, 4 * j_b                   # B[k0 + row][n0 + 4j .. +3]
-    b_lds = (A_STAGE + (wave >> 2) * B_STAGE) * 4 + inst_b * 1024 + lane * 16
+    b_lds = (a_stage + (wave >> 2) * b_stage) * 4 + inst_b * 1024 + lane * 16
     return (a_rows, a_cols, a_lds), (b_rows, b_cols, b_lds)
 
 
 def fusable(m, n, k):
     # gemm_f32_dual_swiglu_fits: whole 128x64 tiles and whole stages.
-    return m % BM == 0 and n % BN == 0 and k % BK == 0 and k > 0
+    return m % 128 == 0 and n % BN == 0 and k % BK == 0 and k > 0
 
 
+def edge_columns(tiles_m, tiles_n):
+    """dual_edge_columns: tile columns that run as 64x64 tiles."""
+    tiles = tiles_m * tiles_n
+    rem = tiles % CUS
+    if tiles <= CUS or rem == 0 or rem > CUS // 2 or rem % tiles_m != 0:
+        return 0
+    return rem // tiles_m
+
+
+def xcd_order(bid, count):
+    per, rem = count // 8, count % 8
+    xcd, idx = bid % 8, bid // 8
+    return xcd * per + np.minimum(xcd, rem) + idx
+
+
+def grouped_tile(logical, tiles_m, tiles_n):
+    span = GROUP_M * tiles_n
+    group = logical // span
+    first = group * GROUP_M
+    rows = np.minimum(tiles_m - first, GROUP_M)
+    inside = logical - group * span
+    return first + inside % rows, inside // rows
+
+
+def tile_origins(m, n):
+    """Workgroup -> (tile height, m0, n0) of the launch (the kernel's blockIdx
+    split and the launcher's grid size)."""
+    tiles_m, tiles_n = m // 128, n // BN
+    edge = edge_columns(tiles_m, tiles_n)
+    body_tn = tiles_n - edge
+    body = tiles_m * body_tn
+    grid = body + 2 * tiles_m * edge
+    bid = np.arange(grid)
+    out = []
+    if body:
+        tm, tn = grouped_tile(xcd_order(bid[:body], body), tiles_m, body_tn)
+        out += [(2, int(a) * 128, int(b) * 64) for a, b in zip(tm, tn)]
+    pos = bid[body:] - body
+    if pos.size:
+        out += [(1, int(a) * 64, int(b) * 64) for a, b in zip(pos // edge, body_tn + pos % edge)]
+    return out, edge
+
+
+@pytest.mark.parametrize("m,n,expect_edge", [(4096, 2816, 4), (2048, 2048, 0), (128, 64, 0), (8192, 2816, 0),
+                                             (1024, 4160, 1), (2048, 2112, 1), (3200, 2816, 0),
+                                             (1152, 2880, 0)])
+def test_fused_tiles_cover_every_output_once(m, n, expect_edge):
+    origins, edge = tile_origins(m, n)
+    assert edge == expect_edge
+    count = np.zeros((m // 64, n // 64), dtype=np.int64)
+    for tm, m0, n0 in origins:
+        assert m0 % 64 == 0 and n0 % 64 == 0 and m0 + 64 * tm <= m and n0 + BN <= n
+        count[m0 // 64:m0 // 64 + tm, n0 // 64] += 1
+    assert (count == 1).all()
+    if edge:
+        # The busiest CU's work drops from ceil(tiles / CUs) to floor + 1/2.
+        tiles = (m // 128) * (n // BN)
+        half = sum(1 for tm, _, _ in origins if tm == 1)
+        assert half == 2 * (tiles % CUS) and half <= CUS
+
+
+@pytest.mark.parametrize("tm", [2, 1])
 @pytest.mark.parametrize("m,n,k", [(4096, 2816, 1024), (2048, 2048, 256), (128, 64, 32), (8192, 2816, 4096)])
-def test_fused_gate_up_swiglu_stays_in_bounds(m, n, k):
+def test_fused_gate_up_swiglu_stays_in_bounds(m, n, k, tm):
     assert fusable(m, n, k)
-    (a_rows, a_cols, a_lds), (b_rows, b_cols, b_lds) = stage_loads()
-    # Every A row and every 16-byte A chunk of the 128x32 stage is loaded once;
+    bm, a_stage, b_stage, stage = shape(tm)
+    (a_rows, a_cols, a_lds), (b_rows, b_cols, b_lds) = stage_loads(tm)
+    # Every A row and every 16-byte A chunk of the stage is loaded once;
     # likewise the 32x64 B stage for each product.
     a_cells = set(zip((a_rows).ravel().tolist(), (a_cols // 4).ravel().tolist()))
-    assert len(a_cells) == BM * BK // 4 == a_rows.size
+    assert len(a_cells) == bm * BK // 4 == a_rows.size
     b_cells = set(zip((b_rows).ravel().tolist(), (b_cols // 4).ravel().tolist()))
     assert len(b_cells) == BK * BN // 4 and b_rows.size == 2 * len(b_cells)  # both products
     # LDS writes: 16 bytes per lane inside the stage, both stages inside 64 KiB.
     for u in (0, 1):
-        lo = u * STAGE * 4 + np.minimum(a_lds.min(), b_lds.min())
-        hi = u * STAGE * 4 + np.maximum(a_lds.max(), b_lds.max()) + 16
-        assert lo >= 0 and hi <= LDS_FLOATS * 4
-    # Global reads over all tiles and stages: A[m0 + row][k0 + col .. col + 3]
-    # and B[k0 + row][n0 + col .. col + 3].
-    m0 = np.arange(0, m, BM)
-    n0 = np.arange(0, n, BN)
+        lo = u * stage * 4 + np.minimum(a_lds.min(), b_lds.min())
+        hi = u * stage * 4 + np.maximum(a_lds.max(), b_lds.max()) + 16
+        assert lo >= 0 and hi <= (u + 1) * stage * 4 <= LDS_FLOATS * 4
+    # Global reads over every tile origin of this height and all stages:
+    # A[m0 + row][k0 + col .. col + 3] and B[k0 + row][n0 + col .. col + 3].
+    origins, _ = tile_origins(m, n)
+    m0 = np.array([o[1] for o in origins if o[0] == tm] or [0])
+    n0 = np.array([o[2] for o in origins if o[0] == tm] or [0])
     k0 = np.arange(0, k, BK)
     a_last = (m0.max() + a_rows.max()) * k + k0.max() + a_cols.max() + 3
     b_last = (k0.max() + b_rows.max()) * n + n0.max() + b_cols.max() + 3
@@ -82,10 +156,12 @@ def test_fused_gate_up_swiglu_stays_in_bounds(m, n, k):
     assert b_rows.min() >= 0 and b_cols.min() >= 0 and b_last < k * n
 
 
-def test_fused_operand_reads_and_hand_off_stay_in_lds():
-    # mma_stage_swz<2, 1> reads of one stage: A rows wm*64 + i*32 + c, chunk
-    # (4h + q) ^ swz_a(row); B row 16h + 4q + e, column wn*32 + c through the
-    # swizzle; the B stage is the group's (gate or up) one.
+@pytest.mark.parametrize("tm", [2, 1])
+def test_fused_operand_reads_and_hand_off_stay_in_lds(tm):
+    # mma_stage_swz<TM, 1> reads of one stage: A rows wm*32*TM + i*32 + c,
+    # chunk (4h + q) ^ swz_a(row); B row 16h + 4q + e, column wn*32 + c
+    # through the swizzle; the B stage is the group's (gate or up) one.
+    bm, a_stage, b_stage, stage = shape(tm)
     lane = np.arange(LANES)
     h, c = lane >> 5, lane & 31
     worst = 0
@@ -93,30 +169,30 @@ def test_fused_operand_reads_and_hand_off_stay_in_lds():
         for wl in range(4):
             wm, wn = wl >> 1, wl & 1
             for q in range(4):
-                for i in range(2):
-                    row = wm * 64 + i * 32 + c
+                for i in range(tm):
+                    row = wm * 32 * tm + i * 32 + c
                     idx = row * BK + (((4 * h + q) ^ swz_a(row)) << 2)
-                    assert idx.min() >= 0 and idx.max() + 4 <= A_STAGE
+                    assert idx.min() >= 0 and idx.max() + 4 <= a_stage
                 for e in range(4):
                     krow = 16 * h + 4 * q + e
                     col = wn * 32 + c
-                    idx = A_STAGE + group * B_STAGE + krow * BN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)
-                    assert idx.min() >= A_STAGE + group * B_STAGE
-                    assert idx.max() < A_STAGE + (group + 1) * B_STAGE
-                    worst = max(worst, int(idx.max()) + STAGE)  # second stage buffer
+                    idx = a_stage + group * b_stage + krow * BN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)
+                    assert idx.min() >= a_stage + group * b_stage
+                    assert idx.max() < a_stage + (group + 1) * b_stage
+                    worst = max(worst, int(idx.max()) + stage)  # second stage buffer
     assert worst < LDS_FLOATS
     # U hand-off: ushare[(i*16 + v)*256 + wl*64 + lane] for the 256 threads of
-    # the up group, then the stores G/U/Act[row][col] of each 128x64 tile.
-    i = np.arange(2)[:, None, None, None]
+    # the up group, then the stores G/U/Act[row][col] of each tile.
+    i = np.arange(tm)[:, None, None, None]
     v = np.arange(16)[None, :, None, None]
     wl = np.arange(4)[None, None, :, None]
     ln = lane[None, None, None, :]
     share = (i * 16 + v) * 256 + wl * 64 + ln
     assert share.min() == 0 and share.max() < LDS_FLOATS and np.unique(share).size == share.size
     wm = wl >> 1
-    rows = wm * 64 + i * 32 + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3)
+    rows = wm * 32 * tm + i * 32 + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3)
     cols = (wl & 1) * 32 + (ln & 31) + 0 * i * v
-    assert rows.min() == 0 and rows.max() == BM - 1 and cols.min() == 0 and cols.max() == BN - 1
+    assert rows.min() == 0 and rows.max() == bm - 1 and cols.min() == 0 and cols.max() == BN - 1
     cells = set(zip(np.broadcast_to(rows, share.shape).ravel().tolist(),
                     np.broadcast_to(cols, share.shape).ravel().tolist()))
-    assert len(cells) == BM * BN  # every output of the tile written exactly once per product
+    assert len(cells) == bm * BN  # every output of the tile written exactly once per product
