@@ -26,7 +26,8 @@ def run_gemm(runtime, m, n, k, a, b, spec_op="gemm", repeats=1):
     ag, bg, out = runtime.resident(a), runtime.resident(b), runtime.alloc(m * n)
     runtime.execute([(kernel, [ag, bg, out])], repeats)
     got = runtime.download(out)
-    assert np.array_equal(runtime.download(ag), a) and np.array_equal(runtime.download(bg), b), "input modified"
+    assert np.array_equal(runtime.download(ag), a, equal_nan=True) and np.array_equal(
+        runtime.download(bg), b, equal_nan=True), "input modified"
     for x in (ag, bg, out):
         x.free()
     return got
@@ -142,6 +143,33 @@ def test_direct_tiles_over_unaligned_rows(runtime, m, n, k, waves):
     b = orc.values(k * n, 0xAB, 1.0)
     got = run_gemm(runtime, m, n, k, a, b, repeats=2)
     gate(got, m, n, k, a, b)
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1000, 777, 513),  # 64x64 tiles, two K groups, unaligned rows: the last stage runs 31 k past K
+    (200, 8, 999),     # K split into slices of 160: a slice's last stage runs into the next slice
+    (500, 777, 513),   # direct-load 32x32 tiles over unaligned rows
+])
+def test_unaligned_rows_keep_non_finite_values_in_place(runtime, m, n, k):
+    # Unaligned loops load whole 32-k runs: past the end of a K range they
+    # read the next A row's first floats or the next slice's B rows. Those
+    # must enter as zeros, so an Inf or NaN there stays in the outputs it
+    # belongs to: A[5][0] = Inf (row 4's run past K reads it), A[7][2] = NaN,
+    # B[160][3] = Inf (the first row of the second K slice at (200, 8, 999)).
+    a = orc.values(m * k, 0xD1, 1.0)
+    b = orc.values(k * n, 0xD2, 1.0)
+    a[5 * k] = np.inf
+    a[7 * k + 2] = np.nan
+    b[160 * n + 3] = np.inf
+    got = run_gemm(runtime, m, n, k, a, b).reshape(m, n)
+    want = orc.gemm_reference(m, n, k, a, b).reshape(m, n)
+    rows = np.setdiff1d(np.arange(m), [5, 7])
+    cols = np.setdiff1d(np.arange(n), [3])
+    clean_got, clean_want = got[np.ix_(rows, cols)], want[np.ix_(rows, cols)]
+    assert np.isfinite(clean_got).all()
+    check = orc.compare(clean_got.reshape(-1), clean_want.reshape(-1), NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, check.first_bad
+    assert not np.isfinite(got[5]).any() and np.isnan(got[7]).all() and not np.isfinite(got[:, 3]).any()
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
