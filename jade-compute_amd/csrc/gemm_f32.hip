@@ -1069,7 +1069,10 @@ struct Slice {
 // offset past any buffer of this kernel, which reads zero without touching
 // memory, so the kernel does not end waiting on loads nobody consumes.
 constexpr uint32_t kDeadOffset = 0x80000000u;
-template <bool BUFA, bool BUFB>
+//
+// WHOLE (K % 32 == 0, with BUFB): every row of every slice lies inside B, so
+// a B row's step is the load's scalar offset and costs no VALU add.
+template <bool BUFA, bool BUFB, bool WHOLE = false>
 __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_rsrc_t ra,
                                   const float *__restrict__ B, __amdgpu_buffer_rsrc_t rb, int K, int N, size_t arow,
                                   int lda, int bcol, int k0, bool live, int h, Slice &s) {
@@ -1090,8 +1093,12 @@ __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_r
         const uint32_t first = live ? (uint32_t(kb) * uint32_t(N) + uint32_t(bcol)) * 4u : kDeadOffset;
         const uint32_t row = uint32_t(N) * 4u;
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-            s.b[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(first + uint32_t(e) * row), 0, 0));
+        for (int e = 0; e < 16; ++e) {
+            if constexpr (WHOLE)
+                s.b[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(first), int(uint32_t(e) * row), 0));
+            else
+                s.b[e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rb, int(first + uint32_t(e) * row), 0, 0));
+        }
     } else {
 #pragma unroll
         for (int e = 0; e < 16; ++e) s.b[e] = B[size_t(min(kb + e, K - 1)) * N + bcol];
@@ -1105,7 +1112,7 @@ __device__ inline void load_slice(const float *__restrict__ A, __amdgpu_buffer_r
 // folded into the running sum with VALU adds, which bounds the length of the
 // matrix cores' accumulation chains for long K ranges.
 constexpr int kChainSlices = 6;
-template <bool ZB, bool CHAIN>
+template <bool ZB, bool CHAIN, bool WHOLE = false>
 __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
     f32x16 part;
 #pragma unroll
@@ -1116,7 +1123,7 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int i = 4 * q + e;
-            const float a = i < valid ? s.a[q][e] : 0.f, b = ZB || i < valid ? s.b[i] : 0.f;
+            const float a = WHOLE || i < valid ? s.a[q][e] : 0.f, b = WHOLE || ZB || i < valid ? s.b[i] : 0.f;
             sum = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, sum, 0, 0, 0);
         }
     if (!CHAIN) acc += part;
@@ -1129,7 +1136,8 @@ __device__ inline void mma_slice(const Slice &s, int valid, f32x16 &acc) {
 // BUFA: A is read through buffer loads, which needs ((M-1)*lda + K)*4 < 2^31
 // (per product of a batch); unaligned rows (K % 4 != 0) require it. BUFB: B
 // is read through buffer loads (K*N*4 < 2^31; per product of a batch).
-template <int G, bool BUFA, bool BUFB, bool CHAIN>
+// WHOLE: K % 32 == 0 and BUFB (no slice runs past K: no masks).
+template <int G, bool BUFA, bool BUFB, bool CHAIN, bool WHOLE = false>
 __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restrict__ A, const float *__restrict__ B,
                                                           float *__restrict__ C, int M, int N, int K, int lda,
                                                           int tiles_m, int tiles_n, size_t sa, size_t sb,
@@ -1167,16 +1175,16 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
     if (count > 0) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            load_slice<BUFA, BUFB>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(d), d < count, h, buf[d]);
+            load_slice<BUFA, BUFB, WHOLE>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(d), d < count, h, buf[d]);
             __builtin_amdgcn_sched_barrier(0);  // loads issued slice by slice
         }
         int i = 0;
         for (; i + D <= count; i += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
-                mma_slice<BUFB, CHAIN>(buf[d], valid(i + d), acc);
-                load_slice<BUFA, BUFB>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(i + d + D), i + d + D < count,
-                                       h, buf[d]);
+                mma_slice<BUFB, CHAIN, WHOLE>(buf[d], valid(i + d), acc);
+                load_slice<BUFA, BUFB, WHOLE>(A, ra, B, rb, K, N, arow, lda, bcol, slice_k(i + d + D),
+                                              i + d + D < count, h, buf[d]);
                 // Keep the slices in order: interleaving their independent
                 // MFMA chains would make the first one wait for every load.
                 __builtin_amdgcn_sched_barrier(0);
@@ -1184,7 +1192,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         }
 #pragma unroll
         for (int d = 0; d < D; ++d)
-            if (i + d < count) mma_slice<BUFB, CHAIN>(buf[d], valid(i + d), acc);
+            if (i + d < count) mma_slice<BUFB, CHAIN, WHOLE>(buf[d], valid(i + d), acc);
     }
     if (G > 1) {
         if (g > 0) {
@@ -1215,7 +1223,9 @@ void launch_direct_gc(hipStream_t stream, dim3 grid, bool bufa, bool bufb, const
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
     };
-    if (bufa)
+    if (bufb && k % kBK == 0)
+        bufa ? go(gemm_f32_direct<G, true, true, CHAIN, true>) : go(gemm_f32_direct<G, false, true, CHAIN, true>);
+    else if (bufa)
         bufb ? go(gemm_f32_direct<G, true, true, CHAIN>) : go(gemm_f32_direct<G, true, false, CHAIN>);
     else
         bufb ? go(gemm_f32_direct<G, false, true, CHAIN>) : go(gemm_f32_direct<G, false, false, CHAIN>);
