@@ -1144,7 +1144,7 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
                                                           size_t sc) {
     using namespace direct;
     constexpr int D = kDepth;
-    __shared__ float red[(G > 1 ? G - 1 : 1) * 16 * 64];
+    __shared__ float red[(G > 1 ? G : 1) * 16 * 64];
     A += blockIdx.y * sa;
     B += blockIdx.y * sb;
     C += blockIdx.y * sc;
@@ -1194,22 +1194,29 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct(const float *__restric
         for (int d = 0; d < D; ++d)
             if (i + d < count) mma_slice<BUFB, CHAIN, WHOLE>(buf[d], valid(i + d), acc);
     }
+    // The G partial tiles meet in LDS; wave g then sums and stores the
+    // accumulator entries v of its share (16/G of them), adding the waves'
+    // partials in wave order.
+    constexpr int kShare = 16 / G;
     if (G > 1) {
-        if (g > 0) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) red[((g - 1) * 16 + v) * 64 + lane] = acc[v];
-        }
+        for (int v = 0; v < 16; ++v) red[(g * 16 + v) * 64 + lane] = acc[v];
         __syncthreads();
-        if (g != 0) return;
 #pragma unroll
-        for (int w = 1; w < G; ++w)
+        for (int j = 0; j < kShare; ++j) {
+            const int v = g * kShare + j;
+            float sum = red[v * 64 + lane];
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[v] += red[((w - 1) * 16 + v) * 64 + lane];
+            for (int w = 1; w < G; ++w) sum += red[(w * 16 + v) * 64 + lane];
+            acc[j] = sum;
+        }
     }
+    const bool interior = tm * 32 + 32 <= M && tn * 32 + 32 <= N;  // wave-uniform
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
+    for (int j = 0; j < kShare; ++j) {
+        const int v = G > 1 ? g * kShare + j : j;
         const int crow = tm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (crow < M && col < N) C[size_t(crow) * N + col] = acc[v];
+        if (interior || (crow < M && col < N)) C[size_t(crow) * N + col] = acc[j];
     }
 }
 
