@@ -654,8 +654,9 @@ struct PairArgs {
 // KG > 1: KG groups of four waves share the workgroup's tile. Group g sums
 // the g-th run of ceil(stages / KG) stages of the workgroup's K range (every
 // group runs that many, so the barriers match; stages past the range read
-// zero), each group with its own double-buffered stages in LDS. Groups
-// 1..KG-1 then leave their sums in LDS and group 0 adds them in group order.
+// zero), each group with its own double-buffered stages in LDS. The groups
+// then leave their sums in LDS and each adds up (in group order) and stores a
+// 1/KG share of the tile.
 // KG = 2 (4) puts two (four) waves on each SIMD where a grid of 64x64 tiles
 // gives each CU one workgroup, so one wave's barrier and LDS waits overlap
 // the others' matrix work. Not used with pair or tail launches.
@@ -665,7 +666,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     int tiles_m, int tiles_n, int kchunk, int tail_base, PairArgs pair) {
     using T = Tile<TM, TN>;
     __shared__ float smem[KG * 2 * T::kStage];
-    static_assert(KG == 1 || (KG - 1) * kThreads * TM * TN * 16 <= KG * 2 * T::kStage,
+    static_assert(KG == 1 || (KG * kThreads * TM * TN * 16 <= KG * 2 * T::kStage && 16 % KG == 0),
                   "group sums must fit in the stage buffers");
     int tm, tn;
     if (pair.tiles > 0) {
@@ -721,46 +722,49 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
-    if (KG > 1) {  // both loops end on a barrier: the stage buffers are free
-        if (group > 0) {
-            float *dst = smem + (group - 1) * TM * TN * 16 * kThreads;
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) dst[((i * TN + j) * 16 + v) * kThreads + t] = acc[i][j][v];
-        }
-        __syncthreads();
-        if (group > 0) return;
-#pragma unroll
-        for (int w = 1; w < KG; ++w) {
-            const float *src = smem + (w - 1) * TM * TN * 16 * kThreads;
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) acc[i][j][v] += src[((i * TN + j) * 16 + v) * kThreads + t];
-        }
-    }
-
     const int h = lane >> 5, c = lane & 31;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * 32 * TN + j * 32 + c;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (PATH == kDmaOnly || (row < M && col < N)) {
-                    const size_t at = size_t(row) * N + col;
-                    out[at] = acc[i][j][v];
-                    if (pair.sum) pair.sum[at] = acc[i][j][v] + pair.residual[at];
-                }
-            }
+    // Entry v of block (i, j) to C (and C + residual when asked).
+    auto put = [&](int i, int j, int v, float x) {
+        const int col = n0 + wn * 32 * TN + j * 32 + c;
+        const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (PATH == kDmaOnly || (row < M && col < N)) {
+            const size_t at = size_t(row) * N + col;
+            out[at] = x;
+            if (pair.sum) pair.sum[at] = x + pair.residual[at];
         }
+    };
+    if constexpr (KG > 1) {
+        // Both loops end on a barrier, so the stage buffers are free: the
+        // groups' sums meet there, and group g then adds and stores entries
+        // [g * 16 / KG, (g + 1) * 16 / KG) of each block, the groups' sums in
+        // group order.
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) smem[(((group * TM + i) * TN + j) * 16 + v) * kThreads + t] = acc[i][j][v];
+        __syncthreads();
+        constexpr int kShare = 16 / KG;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int s = 0; s < kShare; ++s) {
+                    const int v = group * kShare + s;
+                    float x = smem[((i * TN + j) * 16 + v) * kThreads + t];
+#pragma unroll
+                    for (int w = 1; w < KG; ++w) x += smem[(((w * TM + i) * TN + j) * 16 + v) * kThreads + t];
+                    put(i, j, v, x);
+                }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) put(i, j, v, acc[i][j][v]);
     }
 }
 
