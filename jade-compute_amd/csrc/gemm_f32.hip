@@ -723,16 +723,6 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
     const int h = lane >> 5, c = lane & 31;
-    // Entry v of block (i, j) to C (and C + residual when asked).
-    auto put = [&](int i, int j, int v, float x) {
-        const int col = n0 + wn * 32 * TN + j * 32 + c;
-        const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (PATH == kDmaOnly || (row < M && col < N)) {
-            const size_t at = size_t(row) * N + col;
-            out[at] = x;
-            if (pair.sum) pair.sum[at] = x + pair.residual[at];
-        }
-    };
     if constexpr (KG > 1) {
         // Both loops end on a barrier, so the stage buffers are free: the
         // groups' sums meet there, and group g then adds and stores entries
@@ -747,24 +737,42 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         __syncthreads();
         constexpr int kShare = 16 / KG;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * 32 * TN + j * 32 + c;
 #pragma unroll
                 for (int s = 0; s < kShare; ++s) {
                     const int v = group * kShare + s;
                     float x = smem[((i * TN + j) * 16 + v) * kThreads + t];
 #pragma unroll
                     for (int w = 1; w < KG; ++w) x += smem[(((w * TM + i) * TN + j) * 16 + v) * kThreads + t];
-                    put(i, j, v, x);
+                    const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (PATH == kDmaOnly || (row < M && col < N)) {
+                        const size_t at = size_t(row) * N + col;
+                        out[at] = x;
+                        if (pair.sum) pair.sum[at] = x + pair.residual[at];
+                    }
                 }
-    } else {
+            }
+        }
+        return;
+    }
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int j = 0; j < TN; ++j)
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * 32 * TN + j * 32 + c;
 #pragma unroll
-                for (int v = 0; v < 16; ++v) put(i, j, v, acc[i][j][v]);
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (PATH == kDmaOnly || (row < M && col < N)) {
+                    const size_t at = size_t(row) * N + col;
+                    out[at] = acc[i][j][v];
+                    if (pair.sum) pair.sum[at] = acc[i][j][v] + pair.residual[at];
+                }
+            }
+        }
     }
 }
 
