@@ -543,7 +543,12 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // `nk` stages from kbegin; stage kt+2's loads are issued while stage kt is
 // consumed and stage kt+1 (loaded an iteration earlier) is written to LDS.
 // BUF: buffer loads (operands below 2 GiB); else clamped global loads.
-template <int TM, int TN, bool BUF>
+// EARLY: stage k+1 is written to LDS before stage k's MFMAs instead of after
+// them. Measured on two-K-group 64x64 tiles (one workgroup per CU): 1000x777x513
+// 15.73 -> 15.33 us, 1000x777x100 6.57 -> 6.42, 200x8x999 (split K) 10.2 -> 9.9;
+// on one-group tiles (two workgroups per CU) it exposes the loads' latency
+// (3000x3000x3001 508 -> 558 us) and on four groups it was mixed.
+template <int TM, int TN, bool BUF, bool EARLY = false>
 __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float *__restrict__ B, float *smem,
                                         int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
                                         int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
@@ -594,6 +599,11 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
             const int k = kt + u;
             if (k < nk) {  // block-uniform
                 const float *cur = smem + u * T::kStage;
+                // EARLY: stage k+1 goes to the other buffer first (every
+                // wave's reads of it ended before the last barrier), so the
+                // LDS writes run beside this stage's MFMAs rather than between
+                // them and the barrier.
+                if (EARLY && k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
                 // Unconditional, so every path into the loop has the same
                 // loads in flight and the waits below stay exact; stages past
                 // nk load in-bounds (or range-checked) data that is never stored.
@@ -605,7 +615,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 for (int i = 0; i < TM; ++i)
 #pragma unroll
                     for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
-                if (k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
+                if (!EARLY && k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
                 lds_barrier();
             }
         }
@@ -717,8 +727,8 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
-        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane,
-                                                       t, acc);
+        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm,
+                                                                wn, lane, t, acc);
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
