@@ -1018,14 +1018,30 @@ __global__ __launch_bounds__(NW * 64) void attention_pairs_mfma(const float *__r
     };
     // xb's scores alone, the chunk's units interleaved so that two MFMA
     // chains alternate.
+    // Four-wave blocks (one wave per SIMD, no second wave to cover a
+    // dependent MFMA) with one unit per chunk: the two halves of the head dim
+    // run as two MFMA chains, added at the end. Measured: H4 S1024 D128
+    // noncausal 26.5 -> 24.9 us, H16 S512 D128 causal 19.8 -> 19.3; with two
+    // waves per SIMD (head dim 64) it cost 0.5-1%.
     auto scores1 = [&](const KV(&kv)[CH], f32x4(&s_b)[CH]) {
+        if constexpr (CH == 1 && NW == 4) {
+            f32x4 lo = zero4, hi = zero4;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) s_b[c] = zero4;
+            for (int d = 0; d < D4 / 2; ++d) {
+                lo = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[0].k[d >> 2][d & 3], qb[d], lo, 0, 0, 0);
+                const int e = d + D4 / 2;
+                hi = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[0].k[e >> 2][e & 3], qb[e], hi, 0, 0, 0);
+            }
+            s_b[0] = lo + hi;
+        } else {
 #pragma unroll
-        for (int d = 0; d < D4; ++d)
+            for (int c = 0; c < CH; ++c) s_b[c] = zero4;
 #pragma unroll
-            for (int c = 0; c < CH; ++c)
-                s_b[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qb[d], s_b[c], 0, 0, 0);
+            for (int d = 0; d < D4; ++d)
+#pragma unroll
+                for (int c = 0; c < CH; ++c)
+                    s_b[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[c].k[d >> 2][d & 3], qb[d], s_b[c], 0, 0, 0);
+        }
     };
     // `steps` chunks from unit p0, for both query blocks (TWO) or xb alone.
     auto pipeline = [&](int p0, int steps, auto two) {
