@@ -48,6 +48,10 @@ constexpr int kBKV = 64;  // keys per LDS tile (two 32-key sub-tiles)
 constexpr float kLazyMax = 8.0f;
 constexpr uint32_t kMaxSplits = 16;  // key slices per row of a split launch, at most
 constexpr float kLog2e = 1.44269504088896340736f;  // log2(e)
+constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
+// A buffer-load offset past every head of at most 2 GiB: reads zero without
+// touching memory.
+constexpr uint32_t kDeadOffset = 0x80000000u;
 
 // Max and sum over lanes l and l ^ 32 (the two halves of the wave hold the
 // two key halves of a query's scores). v_permlane32_swap exchanges the halves
@@ -95,6 +99,20 @@ __device__ inline void load_rows(const float *__restrict__ X, size_t base, int k
             }
         }
         p[i] = x;
+    }
+}
+
+// VEC: one tensor's rows of a tile through buffer loads over the head
+// (rows past seq lie past the buffer's end and read zero; dims past dim are
+// aimed at kDeadOffset). `lane_off` is the lane's fixed byte offset inside a
+// tile, `tile` the tile's first row times the row bytes.
+template <int DP, int NW>
+__device__ inline void load_rows_buf(__amdgpu_buffer_rsrc_t rsrc, const uint32_t (&lane_off)[AttnShape<DP, NW>::kLoads],
+                                     uint32_t tile, f32x4 (&p)[AttnShape<DP, NW>::kLoads]) {
+#pragma unroll
+    for (int i = 0; i < AttnShape<DP, NW>::kLoads; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, int(lane_off[i] + tile), 0, 0);
+        p[i] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
     }
 }
 
@@ -234,14 +252,49 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
     // and less load both at the tile's start (the split measured 2% slower).
     constexpr bool kSplitStage = DP == 128;
     f32x4 stage[S::kLoads], vstage[kSplitStage ? 1 : S::kLoads];
+    // VEC: K and V rows through buffer loads over the head (below 2 GiB, which
+    // the launcher checks): a fixed byte offset per lane and load plus the
+    // tile's, no bounds branches. Otherwise guarded scalar loads.
+    const uint32_t head_bytes = VEC ? uint32_t(seq) * uint32_t(dim) * 4u : 0u, row_bytes = uint32_t(dim) * 4u;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(K + base), 0, int(head_bytes), int(kRawBuffer));
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(V + base), 0, int(head_bytes), int(kRawBuffer));
+    uint32_t kv_off[S::kLoads];
+#pragma unroll
+    for (int i = 0; i < S::kLoads; ++i) {
+        const int idx = int(threadIdx.x) + i * S::kThreads;
+        const int r = idx / (DP / 4), c4 = (idx % (DP / 4)) * 4;
+        kv_off[i] = c4 < dim ? (uint32_t(r) * uint32_t(dim) + uint32_t(c4)) * 4u : kDeadOffset;
+    }
+    auto fetch = [&](bool is_k, int kt, f32x4(&p)[S::kLoads]) {
+        if constexpr (VEC)
+            load_rows_buf<DP, NW>(is_k ? rk : rv, kv_off, uint32_t(kt) * row_bytes, p);
+        else
+            load_rows<DP, NW, VEC>(is_k ? K : V, base, kt, seq, dim, p);
+    };
+    auto fetch_both = [&](int kt, f32x4(&pk)[S::kLoads], f32x4(&pv)[S::kLoads]) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < S::kLoads; ++i) {
+                const int off = int(kv_off[i] + uint32_t(kt) * row_bytes);
+                const auto a = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+                const auto b = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
+                pk[i] = f32x4{__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]), __uint_as_float(a[3])};
+                pv[i] = f32x4{__uint_as_float(b[0]), __uint_as_float(b[1]), __uint_as_float(b[2]), __uint_as_float(b[3])};
+            }
+        } else {
+            load_kv<DP, NW, VEC>(K, V, base, kt, seq, dim, pk, pv);
+        }
+    };
     if (t_begin < t_end) {  // block-uniform
         if constexpr (kSplitStage) {
-            load_rows<DP, NW, VEC>(K, base, t_begin * kBKV, seq, dim, stage);
+            fetch(true, t_begin * kBKV, stage);
             store_rows<DP, NW>(lds, stage);
-            load_rows<DP, NW, VEC>(V, base, t_begin * kBKV, seq, dim, stage);
+            fetch(false, t_begin * kBKV, stage);
             store_rows<DP, NW>(lds + S::kTile, stage);
         } else {
-            load_kv<DP, NW, VEC>(K, V, base, t_begin * kBKV, seq, dim, stage, vstage);
+            fetch_both(t_begin * kBKV, stage, vstage);
             store_kv<DP, NW>(lds, stage, vstage);
         }
     }
@@ -255,9 +308,9 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         float *next = lds + ((t + 1 - t_begin) & 1) * 2 * S::kTile;
         if (more) {
             if constexpr (kSplitStage)
-                load_rows<DP, NW, VEC>(K, base, kt + kBKV, seq, dim, stage);
+                fetch(true, kt + kBKV, stage);
             else
-                load_kv<DP, NW, VEC>(K, V, base, kt + kBKV, seq, dim, stage, vstage);
+                fetch_both(kt + kBKV, stage, vstage);
         }
         const float *ks = lds + ((t - t_begin) & 1) * 2 * S::kTile;
         const float *vs = ks + S::kTile;
@@ -321,7 +374,7 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         // the registers.
         if (kSplitStage && more) {
             store_rows<DP, NW>(next, stage);
-            load_rows<DP, NW, VEC>(V, base, kt + kBKV, seq, dim, stage);
+            fetch(false, kt + kBKV, stage);
         }
         if (subs > 0) {
             // The online max / normaliser update (log2 domain). The running
@@ -649,7 +702,6 @@ struct Config {
     static constexpr int kWaves = DP == 64 ? 8 : 4, kChunk = 1;
 };
 constexpr int kUnit = 16;  // keys per unit, queries per query block
-constexpr uint32_t kRawBuffer = 0x00020000;  // buffer descriptor word 3: raw buffer, 32-bit data format
 
 template <int DP>
 struct UnitKV {
@@ -1192,7 +1244,8 @@ hipError_t launch_online(hipStream_t stream, const float *q, const float *k, con
     const unsigned q_blocks = (seq + S::kBQ - 1) / S::kBQ;
     const float qscale = (1.0f / sqrtf(float(dim))) * kLog2e;
     const dim3 grid = SPLIT ? dim3(plan.live) : dim3(heads, q_blocks), block(S::kThreads);
-    if (vec)
+    // The vector kernel reads K and V through buffer loads over one head.
+    if (vec && uint64_t(seq) * uint64_t(dim) * 4u < (uint64_t(1) << 31))
         hipLaunchKernelGGL((attention_online_mfma<DP, NW, CAUSAL, true, SPLIT>), grid, block, 0, stream, q, k, v,
                            out, ml, int(seq), int(dim), qscale, int(plan.per), int(heads));
     else

@@ -224,6 +224,24 @@ def test_random_shapes(runtime):
 
 
 @pytest.mark.parametrize("causal", [False, True])
+def test_unsplit_grid_padded_dims_and_ragged_tile(runtime, causal):
+    # The flash kernel's K/V buffer loads: head dim 96 runs in the 128-dim
+    # kernel (the lanes of dims 96-127 read zero from an offset past the
+    # buffer), and seq 1000 ends inside a 64-key tile (rows past seq lie past
+    # the head's buffer and read zero).
+    h, s, d = 32, 1000, 96
+    kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
+    assert kernel.launch["kernel"].startswith("attention_online_mfma_d128"), kernel.launch
+    assert "split" not in kernel.launch["kernel"] and kernel.description["workspace_bytes"] == 0, kernel.launch
+    n = h * s * d
+    q, k, v = orc.normal(n, 0x4141), orc.normal(n, 0x4242), orc.normal(n, 0x4343)
+    got = run_online(runtime, h, s, d, causal, q, k, v)
+    want = orc.attention_reference(h, s, d, causal, q, k, v)
+    check = orc.compare(got, want, NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, (check.first_bad, got[check.first_bad], want[check.first_bad])
+
+
+@pytest.mark.parametrize("causal", [False, True])
 def test_unsplit_four_wave_grid(runtime, causal):
     h, s, d = 32, 1024, 64  # 256 blocks of 128 queries: no key split
     kernel = runtime.compile({"op": "attention_online", "heads": h, "seq": s, "dim": d, "causal": causal})
