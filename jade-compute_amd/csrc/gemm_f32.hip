@@ -56,6 +56,7 @@ constexpr int kThreads = 256;
 constexpr int kBK = 32;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
 constexpr int kGroupM = 8;
+constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
 
 template <int TM, int TN>
 struct Tile {
@@ -126,6 +127,36 @@ __device__ inline void issue_stage_dma(const float *__restrict__ A, const float 
         const int inst = wave * T::kBInst + i;
         const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
         lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
+    }
+}
+
+// Edge tiles of aligned shapes: the same stage through 16-byte buffer loads
+// into LDS (buffer_load_dwordx4 ... lds), whose range check returns zero past
+// the end of A (rows past M) and of B, so no bounds branch is needed. B runs
+// past N read the next row's first columns, which feed only unstored outputs.
+// Whole stages only (k stays below K). `ra` and `rb` cover A and B.
+template <int TM, int TN>
+__device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int N, int K, int m0,
+                                       int n0, int k0, float *stage, int t) {
+    using T = Tile<TM, TN>;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+#pragma unroll
+    for (int i = 0; i < T::kAInst; ++i) {
+        const int inst = wave * T::kAInst + i;
+        const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
+        const uint32_t off = (uint32_t(m0 + row) * uint32_t(K) + uint32_t(k0 + 4 * j)) * 4u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void *)(stage + inst * 256), 16,
+                                                 int(off), 0, 0, 0);
+    }
+    constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
+    float *bstage = stage + T::kAStageS;
+#pragma unroll
+    for (int i = 0; i < T::kBInst; ++i) {
+        const int inst = wave * T::kBInst + i;
+        const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
+        const uint32_t off = (uint32_t(k0 + row) * uint32_t(N) + uint32_t(n0 + 4 * j)) * 4u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (__attribute__((address_space(3))) void *)(bstage + inst * 256),
+                                                 16, int(off), 0, 0, 0);
     }
 }
 
@@ -301,13 +332,24 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
 // group (every group of a workgroup runs the same number of stages, so the
 // barriers match).
-template <int TM, int TN>
+template <int TM, int TN, bool BUF = false>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
                                   int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
-                                  f32x16 (&acc)[TM][TN]) {
+                                  f32x16 (&acc)[TM][TN], int M = 0) {
     using T = Tile<TM, TN>;
     const uint32_t lds0 = lds_address(smem);
-    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin, lds0, t);
+    // BUF: edge tiles, through range-checked buffer loads over A and B.
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(A), 0, BUF ? int(uint32_t(M) * uint32_t(K) * 4u) : 0, int(kBufferWord3));
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(B), 0, BUF ? int(uint32_t(K) * uint32_t(N) * 4u) : 0, int(kBufferWord3));
+    auto issue = [&](int k0, int buf) {
+        if constexpr (BUF)
+            issue_stage_buf<TM, TN>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t);
+        else
+            issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, k0, lds0 + uint32_t(buf * T::kStageS * 4), t);
+    };
+    issue(kbegin, 0);
     drain_vmem();
     __syncthreads();
     // Partial sums run over two stages (64 k) before each fold into acc.
@@ -318,9 +360,7 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
             const int k = kt + u;
             if (k < nk) {  // block-uniform
                 const float *cur = smem + u * T::kStageS;
-                if (k + 1 < nk)
-                    issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
-                                            lds0 + uint32_t((1 - u) * T::kStageS * 4), t);
+                if (k + 1 < nk) issue(kbegin + (k + 1) * kBK, 1 - u);
                 // Raised wave priority while this wave has matrix work, so the
                 // SIMD's arbiter favours it over the co-resident workgroup's
                 // loads and folds (measured +1-2% at 4096^3).
@@ -464,7 +504,6 @@ __device__ inline void store_stage_plain(float *stage, const Regs<TM, TN> &r, in
 // clamped along K or N: a run that crosses the end of a B row reads the next
 // row's first floats into columns past N, which no output keeps, and k >=
 // kend is zeroed when a group's partial last stage is written to LDS.
-constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
 template <int TM, int TN>
 struct BufOffsets {
     uint32_t a[Tile<TM, TN>::kALoads], b[Tile<TM, TN>::kBLoads];
@@ -726,6 +765,13 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && klast - kfirst == KG * nk * kBK;
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
+    // Edge tiles of aligned shapes with whole stages: the same loop through
+    // range-checked buffer loads (operands whose 32-bit offsets, with a tile
+    // of rows past M, stay below 2 GiB).
+    else if (PATH == kMixed && VEC && klast - kfirst == KG * nk * kBK &&
+             (uint64_t(M) + T::kBM) * uint64_t(K) * 4u < (uint64_t(1) << 31) &&
+             (uint64_t(K) + 1) * uint64_t(N) * 4u + T::kBN * 4u < (uint64_t(1) << 31))
+        k_loop_dma<TM, TN, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
         k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm,
                                                                 wn, lane, t, acc);
