@@ -130,6 +130,33 @@ __device__ inline void issue_stage_dma(const float *__restrict__ A, const float 
     }
 }
 
+// Loads [p n / P, (p + 1) n / P) of the n = kAInst + kBInst that
+// issue_stage_dma issues (A's first), for a stage spread over P parts.
+template <int TM, int TN, int P>
+__device__ inline void issue_stage_dma_part(const float *__restrict__ A, const float *__restrict__ B, int N, int K,
+                                            int m0, int n0, int k0, uint32_t stage_lds, int t, int p) {
+    using T = Tile<TM, TN>;
+    constexpr int kN = T::kAInst + T::kBInst;
+    const int lane = t & 63, wave = t >> 6;
+    const float *abase = A + size_t(m0) * K + k0;
+    const float *bbase = B + size_t(k0) * N + n0;
+    const uint32_t sb = stage_lds + T::kAStageS * 4;
+    constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
+#pragma unroll
+    for (int x = 0; x < kN; ++x) {
+        if (x < p * kN / P || x >= (p + 1) * kN / P) continue;  // p is a compile-time index
+        if (x < T::kAInst) {
+            const int inst = wave * T::kAInst + x;
+            const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
+            lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
+        } else {
+            const int inst = wave * T::kBInst + (x - T::kAInst);
+            const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
+            lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
+        }
+    }
+}
+
 // Edge tiles of aligned shapes: the same stage through 16-byte buffer loads
 // into LDS (buffer_load_dwordx4 ... lds), whose range check returns zero past
 // the end of A (rows past M) and of B, so no bounds branch is needed. B runs
@@ -286,9 +313,14 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
 
 // mma_stage over the swizzled layout: A stage at `as`, B stage at `bs`.
 // ZERO: start the sums at zero; otherwise add onto `acc`.
-template <int TM, int TN, bool ZERO = true>
+struct NoHook {
+    __device__ void operator()(int) const {}
+};
+// `hook(q)` runs after quarter q's operand reads are issued and before its
+// MFMAs (the LDS-direct loop issues a share of the next stage's loads there).
+template <int TM, int TN, bool ZERO = true, class Hook = NoHook>
 __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, int wn, int lane,
-                                     f32x16 (&acc)[TM][TN]) {
+                                     f32x16 (&acc)[TM][TN], Hook hook = {}) {
     using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
     if (ZERO) {
@@ -307,21 +339,24 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
             const int row = wm * 32 * TM + i * 32 + c, chunk = 4 * h + q;
             a[i] = *reinterpret_cast<const f32x4 *>(as + row * kBK + ((chunk ^ swz_a(row)) << 2));
         }
+        float b[4][TN];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int krow = 16 * h + 4 * q + e;
-            float b[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int col = wn * 32 * TN + j * 32 + c;
-                b[j] = bs[krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
+                b[e][j] = bs[krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
             }
+        }
+        hook(q);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[j], acc[i][j], 0, 0, 0);
-        }
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[e][j], acc[i][j], 0, 0, 0);
     }
 }
 
@@ -360,15 +395,30 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
             const int k = kt + u;
             if (k < nk) {  // block-uniform
                 const float *cur = smem + u * T::kStageS;
-                if (k + 1 < nk) issue(kbegin + (k + 1) * kBK, 1 - u);
+                const bool more = k + 1 < nk;  // block-uniform
+                // Interior tiles: the next stage's loads spread over the four
+                // quarters of this stage's MFMAs.
+                auto spread = [&](int q) {
+                    if (more)
+                        issue_stage_dma_part<TM, TN, 4>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
+                                                        lds0 + uint32_t((1 - u) * T::kStageS * 4), t, q);
+                };
+                if (BUF && more) issue(kbegin + (k + 1) * kBK, 1 - u);
                 // Raised wave priority while this wave has matrix work, so the
                 // SIMD's arbiter favours it over the co-resident workgroup's
                 // loads and folds (measured +1-2% at 4096^3).
                 __builtin_amdgcn_s_setprio(1);
-                if (u == 0)
-                    mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part);
-                else
-                    mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part);
+                if constexpr (BUF) {
+                    if (u == 0)
+                        mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part);
+                    else
+                        mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part);
+                } else {
+                    if (u == 0)
+                        mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
+                    else
+                        mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
+                }
                 if (u == 1 || k + 1 == nk) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
