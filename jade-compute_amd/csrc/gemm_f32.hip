@@ -54,6 +54,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 constexpr int kBK = 32;
+// Last k of an unaligned K-group tile's range that may add in its epilogue
+// (gemm_f32_mfma) rather than as a stage of their own.
+constexpr int kMaxTail = 2;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
 constexpr int kGroupM = 8;
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
@@ -759,7 +762,7 @@ struct PairArgs {
 // KG = 2 (4) puts two (four) waves on each SIMD where a grid of 64x64 tiles
 // gives each CU one workgroup, so one wave's barrier and LDS waits overlap
 // the others' matrix work. Not used with pair or tail launches.
-template <int TM, int TN, bool VEC, int PATH, int KG = 1>
+template <int TM, int TN, bool VEC, int PATH, int KG = 1, bool KTAIL = false>
 __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(KG > 2 ? KG : 2, KG > 2 ? KG : 2))) void gemm_f32_mfma(
     const float *__restrict__ A, const float *__restrict__ B, float *__restrict__ C, int M, int N, int K,
     int tiles_m, int tiles_n, int kchunk, int tail_base, PairArgs pair) {
@@ -791,11 +794,26 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     const int m0 = tm * T::kBM, n0 = tn * T::kBN;
     const int kfirst = int(blockIdx.y) * kchunk;
     const int klast = min(K, kfirst + kchunk);
+    // KTAIL (unaligned K-group tiles): a K range of whole stages that the
+    // groups split evenly, plus at most kMaxTail last k. Those k would take a
+    // round of their own (a stage of MFMAs on mostly zeros, and its
+    // barriers); they add in the epilogue instead, as rank-1 updates of each
+    // thread's stored outputs from values loaded before the loop.
+    // 1000x777x513 on two groups: 9 rounds per group -> 8. The host picks
+    // KTAIL only when the last K slice has such a tail (ktail_fits).
+    constexpr bool kTail = KTAIL;
+    static_assert(!KTAIL || (KG > 1 && !VEC && TM * TN <= 2), "the tail is for unaligned K-group tiles");
+    int ktail = 0;
+    if constexpr (kTail) {
+        const int whole = (klast - kfirst) / kBK, rest = (klast - kfirst) % kBK;
+        if (whole > 0 && whole % KG == 0 && rest <= kMaxTail) ktail = rest;
+    }
+    const int kmain = klast - ktail;
     const int group = KG > 1 ? __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kThreads) : 0;
     const int t = int(threadIdx.x) % kThreads;
-    const int nk = ((klast - kfirst + kBK - 1) / kBK + KG - 1) / KG;  // stages per group
+    const int nk = ((kmain - kfirst + kBK - 1) / kBK + KG - 1) / KG;  // stages per group
     const int kbegin = kfirst + group * nk * kBK;
-    const int kend = min(klast, kbegin + nk * kBK);
+    const int kend = min(kmain, kbegin + nk * kBK);
     float *gsmem = smem + group * 2 * T::kStage;
     float *__restrict__ out = C + size_t(blockIdx.y) * size_t(M) * size_t(N);
     const int lane = t & 63, wave = t >> 6;
@@ -808,6 +826,31 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+    // The tail's A and B values for the outputs this thread stores (entries
+    // [group * 16 / KG, (group + 1) * 16 / KG) of each block, see the K-group
+    // epilogue), at indices clamped into A and B, issued ahead of the loop's
+    // loads and unconditionally, so every path into the loop has the same
+    // loads in flight.
+    constexpr int kShareT = kTail ? 16 / KG : 1;
+    float ta[kTail ? TM : 1][kShareT][kMaxTail], tb[kTail ? TN : 1][kMaxTail];
+    if constexpr (kTail) {
+        const int h = lane >> 5, c = lane & 31;
+#pragma unroll
+        for (int e = 0; e < kMaxTail; ++e) {
+            const int kk = min(kmain + e, K - 1);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int s = 0; s < kShareT; ++s) {
+                    const int v = group * kShareT + s;
+                    const int row = min(m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3), M - 1);
+                    ta[i][s][e] = A[size_t(row) * K + kk];
+                }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) tb[j][e] = B[size_t(kk) * N + min(n0 + wn * 32 * TN + j * 32 + c, N - 1)];
+        }
+    }
 
     // Interior tiles with 16-byte rows stream through LDS-direct loads; edge
     // tiles, unaligned shapes and K ranges that are not KG x nk whole stages
@@ -853,6 +896,11 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
                     float x = smem[((i * TN + j) * 16 + v) * kThreads + t];
 #pragma unroll
                     for (int w = 1; w < KG; ++w) x += smem[(((w * TM + i) * TN + j) * 16 + v) * kThreads + t];
+                    if constexpr (kTail) {
+#pragma unroll
+                        for (int e = 0; e < kMaxTail; ++e)
+                            if (e < ktail) x = fmaf(ta[i][s][e], tb[j][e], x);
+                    }
                     const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                     if (PATH == kDmaOnly || (row < M && col < N)) {
                         const size_t at = size_t(row) * N + col;
@@ -1679,10 +1727,23 @@ struct Route {
     Path path;             // tile kernel: load path
     bool launchable;
     bool needs_workspace;  // split-K partials go through the caller's workspace
+    bool ktail;            // tile kernel: the last k add in the epilogue (ktail_fits)
 };
 
+// Unaligned K-group tiles (the register-staged loop, at most two blocks per
+// wave) over an unsplit K: whether K is whole stages that the KG groups split
+// evenly plus 1..kMaxTail k, which gemm_f32_mfma's KTAIL variant adds in its
+// epilogue instead of in a round of its own. Split plans keep the partial
+// stage in the loop: their last slice is never the longest, so the tail
+// would not shorten the launch (200x8x1025 measured 9.9 -> 10.4 us with it).
+bool ktail_fits(const Plan &p, bool vec, int kg, uint32_t k) {
+    const uint32_t whole = k / kBK, rest = k % kBK;
+    return !vec && kg > 1 && p.tm * p.tn <= 2 && p.slices == 1 && whole > 0 && whole % uint32_t(kg) == 0 &&
+           rest > 0 && rest <= uint32_t(kMaxTail);
+}
+
 Route route_for(uint32_t m, uint32_t n, uint32_t k) {
-    Route r{plan_for(m, n, k), k % 4 == 0 && n % 4 == 0, 1, kMixed, m > 0 && n > 0 && k > 0, false};
+    Route r{plan_for(m, n, k), k % 4 == 0 && n % 4 == 0, 1, kMixed, m > 0 && n > 0 && k > 0, false, false};
     const Plan &p = r.plan;
     r.needs_workspace = p.slices > 1;
     if (p.big) {
@@ -1698,15 +1759,28 @@ Route route_for(uint32_t m, uint32_t n, uint32_t k) {
     r.kg = p.kgroups == 4 && (r.vec || unaligned_buffers_fit(m, n, k)) ? 4 : p.kgroups >= 2 ? 2 : 1;
     r.path = tile_path(p, r.vec, m, n, k, p.tm, p.tn, r.kg);
     r.launchable = r.launchable && tile_instantiated(p.tm, p.tn, r.kg, r.path, r.vec);
+    r.ktail = r.launchable && ktail_fits(p, r.vec, r.kg, k);
     return r;
 }
 
-template <int TM, int TN, int KG, Path PATH, bool VEC>
+template <int TM, int TN, int KG, Path PATH, bool VEC, bool KTAIL = false>
 hipError_t launch_instance(hipStream_t stream, const Plan &p, dim3 grid, dim3 block, const float *a, const float *b,
                            float *out, uint32_t m, uint32_t n, uint32_t k, const PairArgs &pair) {
-    hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, VEC, PATH, KG>), grid, block, 0, stream, a, b, out, int(m), int(n),
-                       int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
+    hipLaunchKernelGGL((gemm_f32_mfma<TM, TN, VEC, PATH, KG, KTAIL>), grid, block, 0, stream, a, b, out, int(m),
+                       int(n), int(k), p.tiles_m, p.tiles_n, p.kchunk, -1, pair);
     return hipGetLastError();
+}
+
+// Unaligned tiles with TM x TN blocks per wave and KG groups, with or without
+// the epilogue tail.
+template <int TM, int TN, int KG, Path PATH>
+hipError_t launch_unaligned(hipStream_t stream, const Route &r, dim3 grid, dim3 block, const float *a, const float *b,
+                            float *out, uint32_t m, uint32_t n, uint32_t k, const PairArgs &pair) {
+    if constexpr (KG > 1 && TM * TN <= 2)
+        if (r.ktail)
+            return launch_instance<TM, TN, KG, PATH, false, true>(stream, r.plan, grid, block, a, b, out, m, n, k,
+                                                                 pair);
+    return launch_instance<TM, TN, KG, PATH, false>(stream, r.plan, grid, block, a, b, out, m, n, k, pair);
 }
 
 // Launches the four-wave tile kernel for the route's (path, vec) on a
@@ -1724,13 +1798,12 @@ hipError_t launch_tile(hipStream_t stream, const Route &r, const float *a, const
         case kRegOnly: return launch_instance<TM, TN, KG, kRegOnly, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
         case kUnalignedBuf:
             if constexpr (TM * TN <= 2)
-                return launch_instance<TM, TN, KG, kUnalignedBuf, false>(stream, p, grid, block, a, b, out, m, n, k,
-                                                                          pair);
+                return launch_unaligned<TM, TN, KG, kUnalignedBuf>(stream, r, grid, block, a, b, out, m, n, k, pair);
             break;
         case kMixed:
             if (r.vec) return launch_instance<TM, TN, KG, kMixed, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
             if constexpr (KG <= 2)
-                return launch_instance<TM, TN, KG, kMixed, false>(stream, p, grid, block, a, b, out, m, n, k, pair);
+                return launch_unaligned<TM, TN, KG, kMixed>(stream, r, grid, block, a, b, out, m, n, k, pair);
             break;
     }
     return hipErrorInvalidValue;

@@ -146,7 +146,7 @@ def test_direct_tiles_over_unaligned_rows(runtime, m, n, k, waves):
 
 
 @pytest.mark.parametrize("m,n,k", [
-    (1000, 777, 513),  # 64x64 tiles, two K groups, unaligned rows: the last stage runs 31 k past K
+    (1000, 777, 545),  # 64x64 tiles, two K groups, unaligned rows: the last stage runs 31 k past K
     (200, 8, 999),     # K split into slices of 160: a slice's last stage runs into the next slice
     (500, 777, 513),   # direct-load 32x32 tiles over unaligned rows
 ])
@@ -170,6 +170,38 @@ def test_unaligned_rows_keep_non_finite_values_in_place(runtime, m, n, k):
     check = orc.compare(clean_got.reshape(-1), clean_want.reshape(-1), NORTH_STAR_TOL, NORTH_STAR_TOL)
     assert check.status == 0, check.first_bad
     assert not np.isfinite(got[5]).any() and np.isnan(got[7]).all() and not np.isfinite(got[:, 3]).any()
+
+
+@pytest.mark.parametrize("m,n,k,kernel", [
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # 16 whole stages, 8 per group; k = 512 in the epilogue
+    (1000, 777, 514, "gemm_f32_mfma_64x64x32_k2"),  # two tail k
+    (1000, 777, 545, "gemm_f32_mfma_64x64x32_k2"),  # 17 whole stages: the partial stage stays in the loop
+    (1000, 777, 769, "gemm_f32_mfma_64x64x32_k4"),  # 24 whole stages over four groups, one tail k
+    (1000, 777, 1027, "gemm_f32_mfma_64x64x32_k4"),  # three last k: more than the epilogue takes
+    (200, 8, 1025, "gemm_f32_mfma_64x64x32_splitk_k2"),  # split K: the last slice (65 k) keeps its partial stage
+    (300, 300, 2049, "gemm_f32_mfma_64x64x32_splitk_k2"),  # last slice of 129 k
+])
+def test_unaligned_tail_k_in_the_epilogue(runtime, m, n, k, kernel):
+    # Unsplit unaligned K-group tiles whose K is whole stages that the groups
+    # split evenly plus one or two k add those k in the epilogue, from values
+    # loaded before the loop; the other shapes here keep the partial stage in
+    # the loop. Either way an Inf or NaN in the last k reaches its own row or
+    # column only: A[9][K-1] = NaN, B[K-1][5] = Inf.
+    launch = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch
+    assert launch["kernel"] == kernel, launch
+    a = orc.values(m * k, 0xE1, 1.0)
+    b = orc.values(k * n, 0xE2, 1.0)
+    a[9 * k + k - 1] = np.nan
+    b[(k - 1) * n + 5] = np.inf
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2).reshape(m, n)
+    want = orc.gemm_reference(m, n, k, a, b).reshape(m, n)
+    rows = np.setdiff1d(np.arange(m), [9])
+    cols = np.setdiff1d(np.arange(n), [5])
+    clean_got, clean_want = got[np.ix_(rows, cols)], want[np.ix_(rows, cols)]
+    assert np.isfinite(clean_got).all()
+    check = orc.compare(clean_got.reshape(-1), clean_want.reshape(-1), NORTH_STAR_TOL, NORTH_STAR_TOL)
+    assert check.status == 0, check.first_bad
+    assert np.isnan(got[9]).all() and not np.isfinite(got[:, 5]).any()
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
