@@ -632,6 +632,18 @@ __device__ inline void store_stage4_masked(float *stage, const Regs4<TM, TN> &r,
 // The "memory" clobber keeps the compiler from moving memory accesses across.
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// An empty asm statement that reads the register stage `r`: a use of the
+// loaded values on the loop's exit path. Without one, the compiler moves the
+// loads of the first stage of the unrolled pair into the second stage's
+// branch (their only user when the pair is cut short), past the MFMAs they
+// should overlap, so the EARLY store right after waits for their full
+// latency.
+template <class R>
+__device__ inline void keep_live(const R &r) {
+    for (const auto &x : r.a) asm volatile("" ::"v"(x));
+    for (const auto &x : r.b) asm volatile("" ::"v"(x));
+}
+
 // `nk` stages from kbegin; stage kt+2's loads are issued while stage kt is
 // consumed and stage kt+1 (loaded an iteration earlier) is written to LDS.
 // BUF: buffer loads (operands below 2 GiB); else clamped global loads.
@@ -712,6 +724,8 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
             }
         }
     }
+    keep_live(r[0]);
+    keep_live(r[1]);
 }
 
 // Two waves per SIMD (LDS allows two workgroups per CU at the largest tile);
