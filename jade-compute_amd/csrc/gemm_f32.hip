@@ -57,6 +57,10 @@ constexpr int kBK = 32;
 // Last k of an unaligned K-group tile's range that may add in its epilogue
 // (gemm_f32_mfma) rather than as a stage of their own.
 constexpr int kMaxTail = 2;
+// Stages whose products the LDS-direct loops (and the fused gate/up kernel,
+// which must match them bit for bit) sum in MFMA accumulators before each
+// fold into the running sums: 4 stages, 128 k.
+constexpr int kFoldStages = 4;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
 constexpr int kGroupM = 8;
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
@@ -366,8 +370,10 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // The K loop for interior tiles: LDS-direct loads of stage kt+1 run while the
 // matrix cores consume stage kt; each wave drains its own loads, then one
 // barrier publishes the stage and retires the buffer the next loads overwrite.
-// The matrix cores sum two stages into `part` before each fold into acc.
-// `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
+// The matrix cores sum kFoldStages stages into `part` before each fold into
+// acc (four against two: 4096^3 139.0 -> 141.1 TFLOP/s, 2048^3 131.8 ->
+// 133.9; the worst 4096^3 output then uses 20% of the 1e-4 tolerance against
+// 17.5%). `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
 // group (every group of a workgroup runs the same number of stages, so the
 // barriers match).
 template <int TM, int TN, bool BUF = false>
@@ -390,12 +396,12 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
     issue(kbegin, 0);
     drain_vmem();
     __syncthreads();
-    // Partial sums run over two stages (64 k) before each fold into acc.
+    // Partial sums run over kFoldStages stages before each fold into acc.
     f32x16 part[TM][TN];
-    for (int kt = 0; kt < nk; kt += 2) {
+    for (int kt = 0; kt < nk; kt += kFoldStages) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int k = kt + u;
+        for (int uu = 0; uu < kFoldStages; ++uu) {
+            const int k = kt + uu, u = uu & 1;
             if (k < nk) {  // block-uniform
                 const float *cur = smem + u * T::kStageS;
                 const bool more = k + 1 < nk;  // block-uniform
@@ -412,17 +418,17 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 // loads and folds (measured +1-2% at 4096^3).
                 __builtin_amdgcn_s_setprio(1);
                 if constexpr (BUF) {
-                    if (u == 0)
+                    if (uu == 0)
                         mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part);
                     else
                         mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part);
                 } else {
-                    if (u == 0)
+                    if (uu == 0)
                         mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
                     else
                         mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
                 }
-                if (u == 1 || k + 1 == nk) {
+                if (uu == kFoldStages - 1 || k + 1 == nk) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -1022,23 +1028,24 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
     issue_stage<TM>(A, B, N, K, m0, n0, 0, lds0, wave, lane);
     drain_vmem();
     __syncthreads();
-    // The LDS-direct loop's schedule: partial sums over two stages, then a fold.
+    // The LDS-direct loop's schedule: partial sums over kFoldStages stages,
+    // then a fold.
     f32x16 part[TM][1];
-    for (int kt = 0; kt < nk; kt += 2) {
+    for (int kt = 0; kt < nk; kt += kFoldStages) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int k = kt + u;
+        for (int uu = 0; uu < kFoldStages; ++uu) {
+            const int k = kt + uu, u = uu & 1;
             if (k < nk) {
                 const float *cur = smem + u * S::kStage;
                 if (k + 1 < nk)
                     issue_stage<TM>(A, B, N, K, m0, n0, (k + 1) * kBK, lds0 + uint32_t((1 - u) * S::kStage * 4), wave,
                                     lane);
                 __builtin_amdgcn_s_setprio(1);
-                if (u == 0)
+                if (uu == 0)
                     mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
                 else
                     mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
-                if (u == 1 || k + 1 == nk) {
+                if (uu == kFoldStages - 1 || k + 1 == nk) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
                 }
@@ -1510,7 +1517,7 @@ constexpr int kFourGroupMinK = 768;
 //    512x1024x2048 48.3 -> 25.8. A K group needs two stages or more.
 
 // Grids of at least 256 tiles of 256x256 run as 128x128 tiles (two
-// workgroups per CU, each with its own barrier, folding every two stages)
+// workgroups per CU, each with its own barrier, folding every kFoldStages)
 // unless that grid's last round would hold fewer than 128 of its 512
 // workgroups. Measured on MI355X, 128x128 against the 256x256 kernel (plus a
 // tail in smaller tiles): 4096^3 136.6 / 135.2 TFLOP/s, 8192x8192x2048 136.4 /
