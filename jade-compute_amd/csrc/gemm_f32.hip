@@ -658,7 +658,11 @@ __device__ inline void keep_live(const R &r) {
 // 15.73 -> 15.33 us, 1000x777x100 6.57 -> 6.42, 200x8x999 (split K) 10.2 -> 9.9;
 // on one-group tiles (two workgroups per CU) it exposes the loads' latency
 // (3000x3000x3001 508 -> 558 us) and on four groups it was mixed.
-template <int TM, int TN, bool BUF, bool EARLY = false>
+// PAIRS: partial sums over two stages per fold (else one). Measured with two
+// against one: 128x64 tiles 2048x2048x2047 152.5 -> 146.3 us, 2000x1554x1026
+// 80.8 -> 77.3; two K groups 1000x777x513 14.08 -> 13.96; one-group and
+// four-group 64x64 tiles 1.3% slower (3000x3000x3001, 1000x777x1024).
+template <int TM, int TN, bool BUF, bool EARLY = false, bool PAIRS = false>
 __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float *__restrict__ B, float *smem,
                                         int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
                                         int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
@@ -701,8 +705,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
     store(smem, r[0], kbegin);
     lds_barrier();
     // Unrolled by two so the register stage in use is a compile-time index.
-    // Each stage folds its own partial sums (a fold every two stages, as in
-    // the other loops, measured 5% slower here).
+    f32x16 part[TM][TN];
     for (int kt = 0; kt < nk; kt += 2) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -719,12 +722,16 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 // nk load in-bounds (or range-checked) data that is never stored.
                 load(k + 2, r[u]);
                 __builtin_amdgcn_sched_barrier(0);
-                f32x16 part[TM][TN];
-                mma_stage<TM, TN>(cur, wm, wn, lane, part);
+                if (!PAIRS || u == 0)
+                    mma_stage<TM, TN, true>(cur, wm, wn, lane, part);
+                else
+                    mma_stage<TM, TN, false>(cur, wm, wn, lane, part);
+                if (!PAIRS || u == 1 || k + 1 == nk) {
 #pragma unroll
-                for (int i = 0; i < TM; ++i)
+                    for (int i = 0; i < TM; ++i)
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+                        for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
+                }
                 if (!EARLY && k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
                 lds_barrier();
             }
@@ -886,8 +893,8 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
              (uint64_t(K) + 1) * uint64_t(N) * 4u + T::kBN * 4u < (uint64_t(1) << 31))
         k_loop_dma<TM, TN, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
-        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm,
-                                                                wn, lane, t, acc);
+        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2, TM * TN == 2 || KG == 2>(
+            A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
 
