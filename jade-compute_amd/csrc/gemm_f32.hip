@@ -662,7 +662,11 @@ __device__ inline void keep_live(const R &r) {
 // against one: 128x64 tiles 2048x2048x2047 152.5 -> 146.3 us, 2000x1554x1026
 // 80.8 -> 77.3; two K groups 1000x777x513 14.08 -> 13.96; one-group and
 // four-group 64x64 tiles 1.3% slower (3000x3000x3001, 1000x777x1024).
-template <int TM, int TN, bool BUF, bool EARLY = false, bool PAIRS = false>
+// PRIO: raised wave priority over each stage's MFMAs and fold, as in the
+// LDS-direct loop: one-group 64x64 tiles 3000x3000x3001 548 -> 519 us,
+// four groups 1000x777x1024 23.4 -> 22.95; 1-2% slower on two-group and
+// 128x64 tiles.
+template <int TM, int TN, bool BUF, bool EARLY = false, bool PAIRS = false, bool PRIO = false>
 __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float *__restrict__ B, float *smem,
                                         int M, int N, int K, int kbegin, int kend, int nk, int m0, int n0, int wm,
                                         int wn, int lane, int t, f32x16 (&acc)[TM][TN]) {
@@ -722,6 +726,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 // nk load in-bounds (or range-checked) data that is never stored.
                 load(k + 2, r[u]);
                 __builtin_amdgcn_sched_barrier(0);
+                if (PRIO) __builtin_amdgcn_s_setprio(1);
                 if (!PAIRS || u == 0)
                     mma_stage<TM, TN, true>(cur, wm, wn, lane, part);
                 else
@@ -732,6 +737,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 #pragma unroll
                         for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
                 }
+                if (PRIO) __builtin_amdgcn_s_setprio(0);
                 if (!EARLY && k + 1 < nk) store(smem + (1 - u) * T::kStage, r[1 - u], kbegin + (k + 1) * kBK);
                 lds_barrier();
             }
@@ -893,7 +899,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
              (uint64_t(K) + 1) * uint64_t(N) * 4u + T::kBN * 4u < (uint64_t(1) << 31))
         k_loop_dma<TM, TN, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
-        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2, TM * TN == 2 || KG == 2>(
+        k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2, TM * TN == 2 || KG == 2, TM * TN == 1 && KG != 2>(
             A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
     else
         k_loop<TM, TN, VEC, true>(A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
