@@ -114,6 +114,15 @@ __device__ inline uint32_t lds_address(const void *p) {
 __device__ inline int swz_a(int row) { return (row >> 1) & 7; }
 __device__ inline int swz_b(int row) { return row & 7; }
 
+// Tile column of lane c's outputs in MFMA block j of a wave in column wn.
+// With two blocks per wave (TN = 2) the blocks interleave: block j holds the
+// wave's columns 2c + j, so a lane's two B operands of a k row are adjacent
+// and come in one 8-byte LDS read. One block: columns 32 wn + c.
+template <int TN>
+__device__ inline int tile_col(int wn, int j, int c) {
+    return TN == 2 ? wn * 64 + 2 * c + j : wn * 32 * TN + j * 32 + c;
+}
+
 template <int TM, int TN>
 __device__ inline void issue_stage_dma(const float *__restrict__ A, const float *__restrict__ B, int N, int K,
                                        int m0, int n0, int k0, uint32_t stage_lds, int t) {
@@ -289,7 +298,7 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
     using T = Tile<TM, TN>;
     const int h = lane >> 5, c = lane & 31;
     const float *ap = stage + (wm * 32 * TM + c) * kLDA + 16 * h;
-    const float *bp = stage + T::kAStage + (16 * h) * T::kLDB + wn * 32 * TN + c;
+    const float *bp = stage + T::kAStage + (16 * h) * T::kLDB;
     if (ZERO) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
@@ -308,7 +317,7 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
             const int s = 4 * q + e;
             float b[TN];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) b[j] = bp[s * T::kLDB + 32 * j];
+            for (int j = 0; j < TN; ++j) b[j] = bp[s * T::kLDB + tile_col<TN>(wn, j, c)];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -352,7 +361,7 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
             const int krow = 16 * h + 4 * q + e;
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int col = wn * 32 * TN + j * 32 + c;
+                const int col = tile_col<TN>(wn, j, c);
                 b[e][j] = bs[krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
             }
         }
@@ -881,7 +890,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
                     ta[i][s][e] = A[size_t(row) * K + kk];
                 }
 #pragma unroll
-            for (int j = 0; j < TN; ++j) tb[j][e] = B[size_t(kk) * N + min(n0 + wn * 32 * TN + j * 32 + c, N - 1)];
+            for (int j = 0; j < TN; ++j) tb[j][e] = B[size_t(kk) * N + min(n0 + tile_col<TN>(wn, j, c), N - 1)];
         }
     }
 
@@ -922,7 +931,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         for (int i = 0; i < TM; ++i) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                const int col = n0 + wn * 32 * TN + j * 32 + c;
+                const int col = n0 + tile_col<TN>(wn, j, c);
 #pragma unroll
                 for (int s = 0; s < kShare; ++s) {
                     const int v = group * kShare + s;
@@ -949,7 +958,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * 32 * TN + j * 32 + c;
+            const int col = n0 + tile_col<TN>(wn, j, c);
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
