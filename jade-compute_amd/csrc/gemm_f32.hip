@@ -954,6 +954,30 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         }
         return;
     }
+    if constexpr (TN == 2 && VEC) {
+        // The two blocks hold adjacent columns (tile_col): one 8-byte store
+        // per pair, 8-byte aligned since N % 4 == 0.
+        const int col = n0 + tile_col<TN>(wn, 0, c);
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const size_t at = size_t(row) * N + col;
+                if (PATH == kDmaOnly || (row < M && col + 1 < N)) {
+                    *reinterpret_cast<float2 *>(out + at) = make_float2(acc[i][0][v], acc[i][1][v]);
+                    if (pair.sum) {
+                        const float2 r = *reinterpret_cast<const float2 *>(pair.residual + at);
+                        *reinterpret_cast<float2 *>(pair.sum + at) = make_float2(acc[i][0][v] + r.x, acc[i][1][v] + r.y);
+                    }
+                } else if (row < M && col < N) {
+                    out[at] = acc[i][0][v];
+                    if (pair.sum) pair.sum[at] = acc[i][0][v] + pair.residual[at];
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
 #pragma unroll
