@@ -1962,7 +1962,9 @@ bool gemm_f32_residual_fits(uint32_t m, uint32_t n, uint32_t k) {
 
 hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b, float *c, const float *residual,
                              float *sum, uint32_t m, uint32_t n, uint32_t k) {
-    if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum)
+    // The 128x128 epilogue reads the residual and writes the sum in 8-byte pairs.
+    if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum ||
+        !aligned16(residual) || !aligned16(sum))
         return hipErrorInvalidValue;
     PairArgs extra{};
     extra.residual = residual;
