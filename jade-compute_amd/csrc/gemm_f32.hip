@@ -954,29 +954,35 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
         }
         return;
     }
+    // The two blocks hold adjacent columns (tile_col): one 8-byte store per
+    // pair where C (and the residual and sum) start 8-byte aligned; with
+    // N % 4 == 0 every pair then is. Otherwise the single stores below.
     if constexpr (TN == 2 && VEC) {
-        // The two blocks hold adjacent columns (tile_col): one 8-byte store
-        // per pair, 8-byte aligned since N % 4 == 0.
-        const int col = n0 + tile_col<TN>(wn, 0, c);
+        const bool pairs = ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(pair.residual) |
+                             reinterpret_cast<uintptr_t>(pair.sum)) & 7u) == 0;
+        if (pairs) {  // block-uniform
+            const int col = n0 + tile_col<TN>(wn, 0, c);
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
+            for (int i = 0; i < TM; ++i) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                const size_t at = size_t(row) * N + col;
-                if (PATH == kDmaOnly || (row < M && col + 1 < N)) {
-                    *reinterpret_cast<float2 *>(out + at) = make_float2(acc[i][0][v], acc[i][1][v]);
-                    if (pair.sum) {
-                        const float2 r = *reinterpret_cast<const float2 *>(pair.residual + at);
-                        *reinterpret_cast<float2 *>(pair.sum + at) = make_float2(acc[i][0][v] + r.x, acc[i][1][v] + r.y);
+                for (int v = 0; v < 16; ++v) {
+                    const int row = m0 + wm * 32 * TM + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    const size_t at = size_t(row) * N + col;
+                    if (PATH == kDmaOnly || (row < M && col + 1 < N)) {
+                        *reinterpret_cast<float2 *>(out + at) = make_float2(acc[i][0][v], acc[i][1][v]);
+                        if (pair.sum) {
+                            const float2 r = *reinterpret_cast<const float2 *>(pair.residual + at);
+                            *reinterpret_cast<float2 *>(pair.sum + at) =
+                                make_float2(acc[i][0][v] + r.x, acc[i][1][v] + r.y);
+                        }
+                    } else if (row < M && col < N) {
+                        out[at] = acc[i][0][v];
+                        if (pair.sum) pair.sum[at] = acc[i][0][v] + pair.residual[at];
                     }
-                } else if (row < M && col < N) {
-                    out[at] = acc[i][0][v];
-                    if (pair.sum) pair.sum[at] = acc[i][0][v] + pair.residual[at];
                 }
             }
+            return;
         }
-        return;
     }
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -1962,9 +1968,7 @@ bool gemm_f32_residual_fits(uint32_t m, uint32_t n, uint32_t k) {
 
 hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b, float *c, const float *residual,
                              float *sum, uint32_t m, uint32_t n, uint32_t k) {
-    // The 128x128 epilogue reads the residual and writes the sum in 8-byte pairs.
-    if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum ||
-        !aligned16(residual) || !aligned16(sum))
+    if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum)
         return hipErrorInvalidValue;
     PairArgs extra{};
     extra.residual = residual;

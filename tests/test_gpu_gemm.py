@@ -434,3 +434,31 @@ def test_dependent_gemms_keep_order(runtime):
     gate(war["x"], m, n, k, a, b)
     gate(war["c0"], m, n, k, war["x"], b)
     assert np.abs(c0 - war["x"]).max() < 1e-3
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 64), (2500, 2500, 256)])
+def test_output_not_8_byte_aligned_takes_single_stores(runtime, m, n, k):
+    # 128x128 tiles store each lane's two adjacent outputs as one 8-byte write
+    # when C starts 8-byte aligned (always for the runtime's allocations). The
+    # allocation-free entry takes any device C: here C starts 4 bytes into an
+    # allocation, which must take the single stores and give the same bits.
+    import ctypes
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == "gemm_f32_mfma_128x128x32", kernel.launch
+    a = orc.values(m * k, 0xF1, 1.0)
+    b = orc.values(k * n, 0xF2, 1.0)
+    want = run_gemm(runtime, m, n, k, a, b)
+    fn = runtime._lib.jr_gemm_f32_noalloc
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_uint32] * 3 + [ctypes.c_char_p, ctypes.c_size_t]
+    ag, bg, out = runtime.resident(a), runtime.resident(b), runtime.alloc(m * n + 1)
+    err = ctypes.create_string_buffer(1024)
+    print(f"jr_gemm_f32_noalloc {m}x{n}x{k}, C at +4 bytes", flush=True)
+    assert fn(None, ag.ptr, bg.ptr, out.ptr + 4, m, n, k, err, len(err)) == 0, err.value
+    hip = ctypes.CDLL("libamdhip64.so")
+    assert hip.hipDeviceSynchronize() == 0
+    got = runtime.download(out)
+    for x in (ag, bg, out):
+        x.free()
+    assert got[0] == 0.0  # the float before C is untouched (allocations start zeroed)
+    np.testing.assert_array_equal(got[1:], want)
