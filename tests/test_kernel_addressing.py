@@ -196,3 +196,29 @@ def test_fused_operand_reads_and_hand_off_stay_in_lds(tm):
     cells = set(zip(np.broadcast_to(rows, share.shape).ravel().tolist(),
                     np.broadcast_to(cols, share.shape).ravel().tolist()))
     assert len(cells) == bm * BN  # every output of the tile written exactly once per product
+
+
+def tile_col(tn, wn, j, c):
+    """gemm_f32.hip tile_col<TN>: a lane's output column in block j."""
+    return wn * 64 + 2 * c + j if tn == 2 else wn * 32 * tn + j * 32 + c
+
+
+@pytest.mark.parametrize("tn", [1, 2])
+def test_tile_columns_cover_the_tile_once(tn):
+    # Every column of a (64 tn)-wide tile is one lane's output in one block of
+    # one wave column, exactly once; with two blocks (the 128x128 tile) a
+    # lane's two columns are adjacent and start at an even column, so its B
+    # values of a k row are one aligned 8-byte LDS read and its outputs one
+    # 8-byte store (N % 4 == 0).
+    wn, j, c = np.meshgrid(np.arange(2), np.arange(tn), np.arange(32), indexing="ij")
+    cols = tile_col(tn, wn, j, c)
+    assert sorted(cols.ravel().tolist()) == list(range(64 * tn))
+    if tn == 2:
+        assert (cols[:, 1, :] == cols[:, 0, :] + 1).all() and (cols[:, 0, :] % 2 == 0).all()
+        # The B read of row krow, column col sits at chunk (col >> 2) ^ swz_b(krow):
+        # the 32 lanes of a row read 256 contiguous bytes of one 16-chunk group
+        # (all 64 banks once), whatever the row's swizzle.
+        for krow in range(32):
+            for w in range(2):
+                chunks = {((int(x) >> 2) ^ swz_b(krow)) for x in cols[w, 0, :]}
+                assert len(chunks) == 16 and len({ch // 16 for ch in chunks}) == 1
