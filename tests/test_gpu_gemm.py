@@ -178,6 +178,9 @@ def test_unaligned_rows_keep_non_finite_values_in_place(runtime, m, n, k):
     (1000, 777, 545, "gemm_f32_mfma_64x64x32_k2"),  # 17 whole stages: the partial stage stays in the loop
     (1000, 777, 769, "gemm_f32_mfma_64x64x32_k4"),  # 24 whole stages over four groups, one tail k
     (1000, 777, 1027, "gemm_f32_mfma_64x64x32_k4"),  # three last k: more than the epilogue takes
+    (1000, 777, 65, "gemm_f32_mfma_64x64x32_k2"),  # one whole stage per group, then one k
+    (1000, 777, 130, "gemm_f32_mfma_64x64x32_k2"),  # two stages per group, then two k
+    (777, 1000, 1025, "gemm_f32_mfma_64x64x32_k4"),  # eight stages per group of four, then one k
     (200, 8, 1025, "gemm_f32_mfma_64x64x32_splitk_k2"),  # split K: the last slice (65 k) keeps its partial stage
     (300, 300, 2049, "gemm_f32_mfma_64x64x32_splitk_k2"),  # last slice of 129 k
 ])
