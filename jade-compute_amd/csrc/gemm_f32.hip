@@ -414,14 +414,18 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
             if (k < nk) {  // block-uniform
                 const float *cur = smem + u * T::kStageS;
                 const bool more = k + 1 < nk;  // block-uniform
-                // Interior tiles: the next stage's A loads go out after the
-                // first quarter's operand reads, its B loads after the third's.
+                // Interior tiles: the next stage's A loads go out at the top
+                // of this stage, its B loads after the third quarter's operand
+                // reads.
                 auto spread = [&](int q) {
-                    if (more && q % 2 == 0)
+                    if (more && q == 2)
                         issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
-                                                        lds0 + uint32_t((1 - u) * T::kStageS * 4), t, q / 2);
+                                                        lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 1);
                 };
                 if (BUF && more) issue(kbegin + (k + 1) * kBK, 1 - u);
+                if (!BUF && more)
+                    issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
+                                                    lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 0);
                 // Raised wave priority while this wave has matrix work, so the
                 // SIMD's arbiter favours it over the co-resident workgroup's
                 // loads and folds (measured +1-2% at 4096^3).
