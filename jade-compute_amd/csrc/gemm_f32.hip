@@ -1931,14 +1931,16 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     }
     // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
     // run K groups.
+    const uint32_t epilogue_k = r.ktail ? k % kBK : 0;
     if (r.kg == 4)
         return {"gemm_f32_mfma_64x64x32_k4", {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {4 * kThreads, 1, 1},
-                4 * Tile<1, 1>::kLdsBytes};
+                4 * Tile<1, 1>::kLdsBytes, epilogue_k};
     if (r.kg == 2)
         return {p.slices > 1 ? "gemm_f32_mfma_64x64x32_splitk_k2" : "gemm_f32_mfma_64x64x32_k2",
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {2 * kThreads, 1, 1},
-                2 * Tile<1, 1>::kLdsBytes};
+                2 * Tile<1, 1>::kLdsBytes,
+                epilogue_k};
     const int shape = p.tm == 2 ? (p.tn == 2 ? 2 : 1) : 0;
     static const char *names[3][2] = {{"gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_splitk"},
                                       {"gemm_f32_mfma_128x64x32", "gemm_f32_mfma_128x64x32_splitk"},

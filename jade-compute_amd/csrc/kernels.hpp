@@ -17,6 +17,9 @@ struct LaunchShape {
     uint32_t grid[3];
     uint32_t block[3];
     uint32_t lds_bytes;
+    // GEMM K-group tiles over unaligned rows: the last k (1 or 2) that add in
+    // the epilogue rather than in a stage of their own (0 otherwise).
+    uint32_t epilogue_k = 0;
 };
 
 // C[m,n] = A[m,k] * B[k,n], packed row-major FP32, FP32 MFMA accumulate.

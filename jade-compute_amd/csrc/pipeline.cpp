@@ -43,7 +43,8 @@ std::string shape_json(const hipk::LaunchShape &shape) {
     return "{\"kernel\":" + json::quote(shape.kernel) + ",\"grid\":[" + std::to_string(shape.grid[0]) + "," +
            std::to_string(shape.grid[1]) + "," + std::to_string(shape.grid[2]) + "],\"block\":[" +
            std::to_string(shape.block[0]) + "," + std::to_string(shape.block[1]) + "," +
-           std::to_string(shape.block[2]) + "],\"lds_bytes\":" + std::to_string(shape.lds_bytes) + "}";
+           std::to_string(shape.block[2]) + "],\"lds_bytes\":" + std::to_string(shape.lds_bytes) +
+           (shape.epilogue_k ? ",\"epilogue_k\":" + std::to_string(shape.epilogue_k) : std::string()) + "}";
 }
 
 }  // namespace

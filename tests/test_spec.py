@@ -372,3 +372,23 @@ def test_attention_kernel_selection(heads, seq, dim, causal, kernel, blocks):
     d = describe({"op": "attention_online", "heads": heads, "seq": seq, "dim": dim, "causal": causal})
     assert d["launch"]["kernel"] == kernel and d["launch"]["grid"][0] == blocks, d["launch"]
     assert (d["workspace_bytes"] > 0) == kernel.endswith("_split")
+
+
+def test_gemm_epilogue_tail_rule():
+    # Unaligned K-group tiles (two or four groups of four waves, unsplit K) add
+    # the last one or two k in the epilogue when K is whole 32-k stages that
+    # the groups split evenly plus those k; the description reports them as
+    # epilogue_k. Every other plan (aligned rows, split K, other tiles, three
+    # or more last k, stages the groups cannot split evenly) has none.
+    seen = set()
+    for m, n in [(1000, 777), (777, 1000), (200, 8), (1023, 1001), (500, 777), (3000, 3001)]:
+        for k in [33, 65, 66, 67, 97, 129, 130, 257, 513, 514, 515, 545, 769, 770, 1025, 1027, 2049]:
+            launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
+            groups = {512: 2, 1024: 4}.get(launch["block"][0], 1) if "_k" in launch["kernel"] else 1
+            whole, rest = divmod(k, 32)
+            unaligned = k % 4 != 0 or n % 4 != 0
+            want = rest if (unaligned and groups > 1 and launch["grid"][1] == 1 and whole > 0
+                            and whole % groups == 0 and 0 < rest <= 2) else 0
+            assert launch.get("epilogue_k", 0) == want, (m, n, k, launch)
+            seen.add(want)
+    assert seen == {0, 1, 2}
