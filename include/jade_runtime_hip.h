@@ -137,7 +137,10 @@ int jr_fill_normal(float *out, size_t len, uint32_t seed, float mean, float sigm
  * use a static 8 MiB device array that each GPU holds until the process
  * ends, enough for every plan of the current planner; a shape needing more
  * is rejected with code 1. Calls that overlap on one GPU race on that array.
- * Codes as above (1 invalid, 2 runtime). */
+ * The array's device address is looked up by jr_create for its device, or
+ * else by the first call on a device that needs it; a caller that captures
+ * calls into a HIP graph creates a context on that device (or makes one
+ * uncaptured call) first. Codes as above (1 invalid, 2 runtime). */
 int jr_gemm_f32_noalloc(void *stream, const float *a, const float *b, float *c, uint32_t m, uint32_t n, uint32_t k,
                         char *err, size_t cap);
 

@@ -39,6 +39,7 @@
 //  * Other shapes with too few output tiles to fill 256 CUs split K over
 //    gridDim.y: each slice writes a partial product to a workspace and a
 //    reduction kernel sums the slices in slice order (deterministic, no atomics).
+#include "gemm_tiles.hpp"
 #include "kernels.hpp"
 #include "ops.hpp"
 
@@ -49,20 +50,11 @@ namespace jade {
 namespace hipk {
 namespace {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 constexpr int kThreads = 256;
-constexpr int kBK = 32;
 // Last k of an unaligned K-group tile's range that may add in its epilogue
 // (gemm_f32_mfma) rather than as a stage of their own.
 constexpr int kMaxTail = 2;
-// Stages whose products the LDS-direct loops (and the fused gate/up kernel,
-// which must match them bit for bit) sum in MFMA accumulators before each
-// fold into the running sums: 4 stages, 128 k.
-constexpr int kFoldStages = 4;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
-constexpr int kGroupM = 8;
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
 
 template <int TM, int TN>
@@ -81,38 +73,6 @@ struct Tile {
     static_assert(kStageS <= kStage, "swizzled stage must fit in the padded stage allocation");
     static constexpr uint32_t kLdsBytes = 2u * kStage * sizeof(float);
 };
-
-// ---- LDS-direct staging --------------------------------------------------
-// global_load_lds_dwordx4 moves 16 bytes per lane straight from global memory
-// into LDS at M0 + lane*16, with no staging registers and no ds_write. It is
-// issued through inline asm with a zero immediate offset: the hardware adds
-// the immediate to both the global and the LDS address. Both bases are
-// wave-uniform and are moved to SGPRs explicitly. The loads are counted by
-// vmcnt, which the caller drains before the barrier that publishes a stage.
-__device__ inline void lds_dma16(const float *base, uint32_t voff, uint32_t lds_addr) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(b));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(uint32_t(b >> 32));
-    const float *ub = reinterpret_cast<const float *>((uint64_t(hi) << 32) | lo);
-    const uint32_t ul = __builtin_amdgcn_readfirstlane(lds_addr);
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1\n" ::"v"(voff), "s"(ub), "s"(ul)
-                 : "memory");
-}
-__device__ inline void drain_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-__device__ inline uint32_t lds_address(const void *p) {
-    return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)p));
-}
-
-// Swizzled stage layout: row r of a stage is unpadded and its 16-byte chunk j
-// sits at chunk position j ^ swz(r). An A operand read (ds_read_b128) serves 16
-// lanes per cycle from 256 bytes of banks; those lanes read 16 consecutive
-// 128-byte rows at one logical chunk, and swz_a = (r >> 1) & 7 gives the eight
-// even and the eight odd rows eight distinct 16-byte slots each. (r & 7) left
-// rows r and r+8 on the same banks: SQ_LDS_BANK_CONFLICT counted 4 cycles per
-// read.) B operand reads cover 32 consecutive columns of one row per half-wave,
-// which the XOR keeps inside one 128-byte group. Neither read needs padding.
-__device__ inline int swz_a(int row) { return (row >> 1) & 7; }
-__device__ inline int swz_b(int row) { return row & 7; }
 
 // Tile column of lane c's outputs in MFMA block j of a wave in column wn.
 // With two blocks per wave (TN = 2) the blocks interleave: block j holds the
@@ -201,25 +161,6 @@ __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffe
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (__attribute__((address_space(3))) void *)(bstage + inst * 256),
                                                  16, int(off), 0, 0, 0);
     }
-}
-
-// Position of block `bid` among `count` when each XCD (blocks go round-robin
-// over the 8 XCDs by id) owns a contiguous range of positions.
-__device__ inline int xcd_order(int bid, int count) {
-    const int per = count / 8, rem = count % 8;
-    const int xcd = bid % 8, idx = bid / 8;
-    return xcd * per + min(xcd, rem) + idx;
-}
-
-// Grouped tile order: kGroupM tile rows at a time, column-major inside a group.
-__device__ inline void grouped_tile(int logical, int tiles_m, int tiles_n, int &tm, int &tn) {
-    const int group_span = kGroupM * tiles_n;
-    const int group = logical / group_span;
-    const int first_m = group * kGroupM;
-    const int group_rows = min(tiles_m - first_m, kGroupM);
-    const int in_group = logical - group * group_span;
-    tm = first_m + in_group % group_rows;
-    tn = in_group / group_rows;
 }
 
 __device__ inline void tile_coords(int tiles_m, int tiles_n, int &tm, int &tn) {
@@ -1507,12 +1448,16 @@ hipError_t launch_direct(hipStream_t stream, dim3 grid, int g, bool bufa, const 
     return hipGetLastError();
 }
 
-// C[i] = sum over slices z (in order) of W[z*MN + i].
+// C[i] = sum over slices z (in order) of W[z*MN + i]. 16-byte runs only
+// where every run of W and of C is 16-byte aligned: mn % 4 == 0 and both
+// bases aligned (W is a whole workspace; C may start at any 4-byte boundary,
+// as the allocation-free entry accepts).
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ W, float *__restrict__ C,
                                                      size_t mn, int slices) {
     const size_t i = (size_t(blockIdx.x) * 256 + threadIdx.x) * 4;
     if (i >= mn) return;
-    if (i + 4 <= mn && mn % 4 == 0) {
+    const bool runs = mn % 4 == 0 && ((reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(C)) & 15u) == 0;
+    if (i + 4 <= mn && runs) {
         f32x4 s = *reinterpret_cast<const f32x4 *>(W + i);
         for (int z = 1; z < slices; ++z) s += *reinterpret_cast<const f32x4 *>(W + size_t(z) * mn + i);
         *reinterpret_cast<f32x4 *>(C + i) = s;
@@ -1536,6 +1481,7 @@ struct Plan {
     int kgroups;    // 2 or 4: 64x64 tiles with that many K groups of four waves (0 or 1: one group)
     int tail_tm, tail_tn;  // big plans: the partial last round's tile, (64*tail_tm) x (64*tail_tn)
     bool bufa;             // direct plans over unaligned A rows: A through buffer loads
+    bool ring = false;     // persistent 128x128 tiles, one workgroup per CU (gemm_f32_ring)
 };
 
 constexpr int kSlots = 512;        // co-resident 256-thread workgroups: two per CU
@@ -1703,7 +1649,48 @@ int direct_waves_unaligned(uint32_t m, uint32_t n, uint32_t k) {
     return g;
 }
 
+// Persistent 128x128 tiles (gemm_f32_ring): whole tiles, K in whole
+// eight-stage iterations, at least one tile per CU, 32-bit load offsets
+// (with the stores' row offsets inside a tile).
+bool ring_fits(uint32_t m, uint32_t n, uint32_t k) {
+    if (m % ring::kBM != 0 || n % ring::kBN != 0 || k % (kBK * ring::kUnroll) != 0 || k == 0) return false;
+    if (!dma_offsets_fit(ring::kBM, ring::kBN, k, n)) return false;
+    return uint64_t(m / ring::kBM) * (n / ring::kBN) >= uint64_t(kCUs);
+}
+
+Plan plan_tiles(uint32_t m, uint32_t n, uint32_t k);
+
+// The persistent kernel replaces the tile plans where it fits and K is at
+// least 512, when the plan it replaces uses 128x128 or 256x256 tiles (those
+// share its tile and its imbalance), or when its grid keeps the CUs busy: the
+// busiest CU holds ceil(t / 256) of the t tiles, at most 1/0.9 of the average.
+// Measured on MI355X against the tile plans (TFLOP/s): 4096^3 141.6 -> 149.3,
+// 4096x11008x4096 138.6 -> 146.4, 5120x5120x2048 127.5 -> 131.9 (256x256
+// tiles and a tail before), 4352x4096x1024 110.4 -> 122.7, 2560^3 109.5 ->
+// 114.6 (400 tiles), 4608^2x1024 117.2 -> 124.1; over 128x64 tiles 2048^3
+// 131.0 -> 138.3 (256 tiles), 4096x1024x2816 131.4 -> 141.2, 4096x2816x1024
+// (704) 120.8 -> 129.3, 12288x1024x1024 (768) 132.1 -> 140.6, 1024x4096x4096
+// 135.7 -> 145.9. Grids of 384 and 576 tiles lost to the smaller tiles
+// (6144x1024x1024 127.5 -> 104.8, 1536x4096x4096 133.3 -> 110.9, 3072^3 on
+// 64x64 tiles 118.0 -> 111.7), as did K = 256 (one iteration per tile:
+// 4096x4096x256 119.6 -> 118.0).
+bool ring_takes(uint32_t m, uint32_t n, uint32_t k, const Plan &tiles) {
+    if (!ring_fits(m, n, k) || k < 512) return false;
+    if (tiles.big || (tiles.tm == 2 && tiles.tn == 2)) return true;
+    const uint64_t t = uint64_t(m / ring::kBM) * (n / ring::kBN), rounds = (t + kCUs - 1) / kCUs;
+    return 10 * t >= 9 * rounds * uint64_t(kCUs);
+}
+
 Plan plan_for(uint32_t m, uint32_t n, uint32_t k) {
+    const Plan p = plan_tiles(m, n, k);
+    if (!ring_takes(m, n, k, p)) return p;
+    Plan r{2, 2, 1, int(k), int(m / ring::kBM), int(n / ring::kBN), false, 0, 0, 1, 0, 0};
+    r.ring = true;
+    return r;
+}
+
+// The plan among the non-persistent kernels.
+Plan plan_tiles(uint32_t m, uint32_t n, uint32_t k) {
     if (big_fits(m, n, k)) {
         const int tiles = int((m / big::kBM) * (n / big::kBN));
         if ((4 * tiles) % kSlots == 0 || (4 * tiles) % kSlots >= kSlots / 4)
@@ -1823,8 +1810,8 @@ Route route_for(uint32_t m, uint32_t n, uint32_t k) {
     Route r{plan_for(m, n, k), k % 4 == 0 && n % 4 == 0, 1, kMixed, m > 0 && n > 0 && k > 0, false, false};
     const Plan &p = r.plan;
     r.needs_workspace = p.slices > 1;
-    if (p.big) {
-        r.launchable = r.launchable && r.vec;  // big_fits implies n % 256 == 0 and k % 32 == 0
+    if (p.big || p.ring) {
+        r.launchable = r.launchable && r.vec;  // big_fits / ring_fits imply n % 128 == 0 and k % 32 == 0
         return r;
     }
     if (p.direct) {
@@ -1912,6 +1899,11 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
     const Route r = route_for(m, n, k);
     const Plan &p = r.plan;
     if (!r.launchable) return {nullptr, {0, 0, 0}, {0, 0, 0}, 0};
+    if (p.ring)
+        return {"gemm_f32_ring_128x128x32",
+                {uint32_t(std::min(p.tiles_m * p.tiles_n, kCUs)), 1, 1},
+                {ring::kThreads, 1, 1},
+                ring::kLdsBytes};
     if (p.big) {  // the first launch; a partial last round follows as smaller tiles
         const char *name = "gemm_f32_mfma_256x256x32";
         if (p.big_full < p.tiles_m * p.tiles_n)
@@ -1927,7 +1919,7 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
         return {p.slices > 1 ? "gemm_f32_direct_32x32x32_w4_splitk" : p.bufa ? buf_names[w] : names[w],
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {uint32_t(64 * p.direct), 1, 1},
-                uint32_t(p.direct > 1 ? (p.direct - 1) * 16 * 64 * sizeof(float) : 0)};
+                uint32_t((p.direct > 1 ? p.direct : 1) * 16 * 64 * sizeof(float))};  // gemm_f32_direct's red[]
     }
     // Otherwise 128x128, 128x64 or 64x64 tiles; only 64x64 tiles split K or
     // run K groups.
@@ -1955,7 +1947,7 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
 
 bool gemm_f32_pairable(uint32_t m, uint32_t n, uint32_t k) {
     const Route r = route_for(m, n, k);
-    return r.launchable && !r.plan.big && !r.plan.direct && r.kg == 1 && r.plan.slices == 1;
+    return r.launchable && !r.plan.big && !r.plan.ring && !r.plan.direct && r.kg == 1 && r.plan.slices == 1;
 }
 
 hipError_t gemm_f32_pair(hipStream_t stream, const float *a0, const float *b0, float *c0, const float *a1,
@@ -1976,19 +1968,25 @@ hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b,
                              float *sum, uint32_t m, uint32_t n, uint32_t k) {
     if (!gemm_f32_residual_fits(m, n, k) || !aligned16(a) || !aligned16(b) || !residual || !sum)
         return hipErrorInvalidValue;
+    const Route r = route_for(m, n, k);
+    if (r.plan.ring)
+        return launch_gemm_ring(stream, a, b, c, n, k, r.plan.tiles_m, r.plan.tiles_n,
+                                unsigned(std::min(r.plan.tiles_m * r.plan.tiles_n, kCUs)), residual, sum);
     PairArgs extra{};
     extra.residual = residual;
     extra.sum = sum;
-    return launch_route_tiles(stream, route_for(m, n, k), a, b, c, m, n, k, extra);
+    return launch_route_tiles(stream, r, a, b, c, m, n, k, extra);
 }
 
 bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
-    // The plan the pair would take must be the 128x64 tile, so the fused
-    // outputs are the pair's bits.
+    // The plan each product would take alone must give the fused kernel's
+    // bits: the 128x64 tile (paired), or the persistent kernel, whose outputs
+    // take the same MFMA steps over k and the same folds per output.
     const Route r = route_for(m, n, k);
     const Plan &p = r.plan;
-    return gemm_f32_pairable(m, n, k) && p.tm == 2 && p.tn == 1 && m % dual::T::kBM == 0 && n % dual::T::kBN == 0 &&
-           k % kBK == 0 && dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
+    const bool same_bits = r.launchable && (p.ring || (gemm_f32_pairable(m, n, k) && p.tm == 2 && p.tn == 1));
+    return same_bits && m % dual::T::kBM == 0 && n % dual::T::kBN == 0 && k % kBK == 0 &&
+           dma_offsets_fit(dual::T::kBM, dual::T::kBN, k, n);
 }
 
 // Tile columns at the right edge that the fused launch runs as 64x64 tiles:
@@ -2032,6 +2030,10 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
     const Route r = route_for(m, n, k);
     if (!r.launchable || (r.needs_workspace && !workspace)) return hipErrorInvalidValue;
     const Plan &p = r.plan;
+    if (p.ring) {
+        return launch_gemm_ring(stream, a, b, c, n, k, p.tiles_m, p.tiles_n,
+                                unsigned(std::min(p.tiles_m * p.tiles_n, kCUs)));
+    }
     if (p.big) {
         hipLaunchKernelGGL(gemm_f32_mfma_256, dim3(unsigned(p.big_full)), dim3(big::kThreads), 0, stream, a, b, c,
                            int(m), int(n), int(k), p.tiles_m, p.tiles_n);

@@ -22,6 +22,10 @@ struct LaunchShape {
     uint32_t epilogue_k = 0;
 };
 
+// jr_gemm_f32_noalloc's set-up on `device` (current): looks up and keeps the
+// device address of its static scratch array. Throws dev::Refusal on failure.
+void noalloc_prepare(int device);
+
 // C[m,n] = A[m,k] * B[k,n], packed row-major FP32, FP32 MFMA accumulate.
 // Small output grids split K; they need `gemm_f32_workspace_bytes` of device
 // workspace (0 when the shape does not split), passed as `workspace`.

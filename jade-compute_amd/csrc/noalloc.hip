@@ -8,7 +8,9 @@
 // file-scope device array of kScratchBytes that every GPU the library runs on
 // holds until the process ends. Its device address differs per GPU and is
 // looked up once per device with hipGetSymbolAddress (the array's name is a
-// host-side stand-in, not a device address). Every call on one GPU shares
+// host-side stand-in, not a device address); creating a runtime context on a
+// device (jr_create) does that lookup, so calls on that device made later,
+// for example under stream capture, only read the kept address. Every call on one GPU shares
 // that GPU's array: calls that overlap on one GPU (two streams, or two
 // threads) race on it. No clearing is needed: each split slice writes every
 // element the reduce reads.
@@ -48,6 +50,19 @@ float *scratch_on(int device) {
     }
     return g_scratch[device];
 }
+
+}  // namespace
+
+namespace jade {
+namespace hipk {
+// Looks up this device's address of the scratch array (the device must be
+// current). jr_create calls it for its device, so that calls made later
+// under stream capture need no lookup there.
+void noalloc_prepare(int device) { (void)scratch_on(device); }
+}  // namespace hipk
+}  // namespace jade
+
+namespace {
 
 int jr_code(jade::dev::Kind kind) {
     return kind == jade::dev::Kind::Invalid ? 1 : kind == jade::dev::Kind::Memory ? 3 : 2;

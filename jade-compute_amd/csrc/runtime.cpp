@@ -201,6 +201,10 @@ extern "C" int jr_create(int device, void **out, char *err, size_t cap) {
     return entry(err, cap, [&] {
         if (!out) refuse_invalid("jr_create needs somewhere to return the handle");
         std::unique_ptr<RuntimeContext> c(new RuntimeContext(device));
+        // The allocation-free GEMM's per-device scratch address, looked up
+        // here (the context's device is current) rather than inside a call
+        // that may run under stream capture.
+        jade::hipk::noalloc_prepare(device);
         g_contexts.add(c.get());
         *out = c.release();
     });

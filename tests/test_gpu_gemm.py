@@ -465,3 +465,57 @@ def test_output_not_8_byte_aligned_takes_single_stores(runtime, m, n, k):
         x.free()
     assert got[0] == 0.0  # the float before C is untouched (allocations start zeroed)
     np.testing.assert_array_equal(got[1:], want)
+
+
+@pytest.mark.parametrize("m,n,k,rows", [
+    (2048, 2048, 512, None),       # 256 tiles: one per workgroup, 16 stages
+    (2560, 2560, 1024, None),      # 400 tiles: runs of one and two tiles
+    (4096, 2816, 1024, None),      # 704 tiles: runs of two and three (the MLP gate/up shape)
+    (4096, 1024, 2816, None),      # the MLP down projection: K of 11 iterations
+    (3840, 3840, 2048, (1792, 2304)),  # 900 tiles: runs of three and four
+    (4096, 4096, 512, (0, 640)),   # 1024 tiles: four per workgroup
+    (12288, 1024, 1024, (11264, 12288)),
+])
+def test_persistent_ring_shapes(runtime, m, n, k, rows):
+    # Persistent 128x128 tiles (gemm_ring.hip): every workgroup runs its tiles
+    # as one sequence of stages, so tile boundaries, the stores of the
+    # previous tile and runs of unequal length are all inside one launch.
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == "gemm_f32_ring_128x128x32" and kernel.launch["grid"][0] == 256, kernel.launch
+    a = orc.values(m * k, 0x9A, 1.0)
+    b = orc.values(k * n, 0x9B, 1.0)
+    print(f"ring {m}x{n}x{k}", flush=True)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    if rows is None:
+        gate(got, m, n, k, a, b)
+    else:
+        gate(got, m, n, k, a, b, rows)
+        gate(got, m, n, k, a, b, (0, 128))
+        gate(got, m, n, k, a, b, (m - 128, m))
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 2048, 512), (2560, 2560, 1024)])
+def test_persistent_ring_output_not_8_byte_aligned(runtime, m, n, k):
+    # The persistent kernel stores pairs of adjacent outputs as one 8-byte
+    # write when C (and a residual) start 8-byte aligned; C at +4 bytes
+    # through the allocation-free entry takes single stores, same bits.
+    import ctypes
+    kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
+    assert kernel.launch["kernel"] == "gemm_f32_ring_128x128x32", kernel.launch
+    a = orc.values(m * k, 0xF3, 1.0)
+    b = orc.values(k * n, 0xF4, 1.0)
+    want = run_gemm(runtime, m, n, k, a, b)
+    fn = runtime._lib.jr_gemm_f32_noalloc
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_uint32] * 3 + [ctypes.c_char_p, ctypes.c_size_t]
+    ag, bg, out = runtime.resident(a), runtime.resident(b), runtime.alloc(m * n + 1)
+    err = ctypes.create_string_buffer(1024)
+    print(f"jr_gemm_f32_noalloc ring {m}x{n}x{k}, C at +4 bytes", flush=True)
+    assert fn(None, ag.ptr, bg.ptr, out.ptr + 4, m, n, k, err, len(err)) == 0, err.value
+    hip = ctypes.CDLL("libamdhip64.so")
+    assert hip.hipDeviceSynchronize() == 0
+    got = runtime.download(out)
+    for x in (ag, bg, out):
+        x.free()
+    assert got[0] == 0.0
+    np.testing.assert_array_equal(got[1:], want)

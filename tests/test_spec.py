@@ -157,10 +157,11 @@ def test_constant_bits_round_trip():
 
 
 @pytest.mark.parametrize("m,n,k,kernel,grid", [
-    (4096, 4096, 4096, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # >= 256 tiles of 256x256: whole 128x128 rounds
-    (8192, 8192, 256, "gemm_f32_mfma_128x128x32", [4096, 1, 1]),
+    (4096, 4096, 4096, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # persistent 128x128 tiles, one workgroup per CU
+    (8192, 8192, 256, "gemm_f32_mfma_128x128x32", [4096, 1, 1]),  # K < 512 keeps the tile kernel
     (4096, 4096, 4112, "gemm_f32_mfma_128x128x32", [1024, 1, 1]),  # K not a multiple of 32
-    (2048, 2048, 2048, "gemm_f32_mfma_128x64x32", [512, 1, 1]),
+    (2048, 2048, 2048, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # one tile per CU
+    (2048, 2048, 2080, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # K not a multiple of 256
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, K >= 768: four K groups
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2", [256, 1, 1]),  # shorter K: two K groups
     (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k4", [208, 1, 1]),  # unaligned rows through buffer loads: four too
@@ -178,24 +179,33 @@ def test_constant_bits_round_trip():
     (1024, 512, 1024, "gemm_f32_mfma_64x64x32_splitk_k2", [128, 2, 1]),  # 8 slices per wave: split K
     (512, 512, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [64, 4, 1]),
     (256, 256, 4096, "gemm_f32_mfma_64x64x32_splitk_k2", [16, 16, 1]),
-    (4096, 11008, 4096, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),  # 128x128 last round 192/512 full
-    (5120, 5120, 2048, "gemm_f32_mfma_256x256x32_tail64x64", [256, 1, 1]),  # 128x128 last round 64/512: 256x256 + tail
-    (4352, 4096, 1024, "gemm_f32_mfma_256x256x32_tail128x128", [256, 1, 1]),  # tail 16: one 128x128 per CU
-    (6144, 6144, 1024, "gemm_f32_mfma_128x128x32", [2304, 1, 1]),
+    (4096, 11008, 4096, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # 10.75 tiles per workgroup
+    (4096, 11008, 4128, "gemm_f32_mfma_128x128x32", [2752, 1, 1]),  # 128x128 last round 192/512 full
+    (5120, 5120, 2048, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # replaces 256x256 + tail
+    (5120, 5120, 2080, "gemm_f32_mfma_256x256x32_tail64x64", [256, 1, 1]),  # 128x128 last round 64/512: 256x256 + tail
+    (4352, 4096, 1056, "gemm_f32_mfma_256x256x32_tail128x128", [256, 1, 1]),  # tail 16: one 128x128 per CU
+    (6144, 6144, 1024, "gemm_f32_ring_128x128x32", [256, 1, 1]),
+    (6144, 6144, 1056, "gemm_f32_mfma_128x128x32", [2304, 1, 1]),
     (3072, 3072, 3072, "gemm_f32_mfma_64x64x32", [2304, 1, 1]),  # 128x128 would fill 56% of two rounds
     (2500, 2500, 2500, "gemm_f32_mfma_128x128x32", [400, 1, 1]),
-    (1024, 4096, 4096, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # 128x64 also for wide C
-    (6144, 1024, 1024, "gemm_f32_mfma_128x64x32", [768, 1, 1]),  # edge-free, 3 tiles per CU against 6 half-size
+    (1024, 4096, 4096, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # 256 tiles: balanced
+    (1024, 4096, 4128, "gemm_f32_mfma_128x64x32", [512, 1, 1]),  # 128x64 also for wide C
+    (6144, 1024, 1024, "gemm_f32_mfma_128x64x32", [768, 1, 1]),  # 384 persistent tiles: 1.5 per CU, kept
     (2048, 3072, 1024, "gemm_f32_mfma_128x64x32", [768, 1, 1]),
     (2048, 3072, 384, "gemm_f32_mfma_64x64x32", [1536, 1, 1]),  # K < 512 keeps the smaller tile
     (3072, 1024, 4096, "gemm_f32_mfma_64x64x32", [768, 1, 1]),  # 3 tiles per CU against 2 of twice the size
     (3648, 3648, 1024, "gemm_f32_mfma_64x64x32", [3249, 1, 1]),  # 128x128 would leave edge tiles
-    (12288, 1024, 1024, "gemm_f32_mfma_128x64x32", [1536, 1, 1]),  # 128x128 predicted < 5% faster: kept
-    (4096, 2816, 1024, "gemm_f32_mfma_128x64x32", [1408, 1, 1]),  # MLP gate/up
+    (12288, 1024, 1024, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # 768 persistent tiles: balanced
+    (12288, 1024, 1056, "gemm_f32_mfma_128x64x32", [1536, 1, 1]),  # 128x128 predicted < 5% faster: kept
+    (4096, 2816, 1024, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # MLP gate/up alone (704 tiles)
+    (4096, 1024, 2816, "gemm_f32_ring_128x128x32", [256, 1, 1]),  # MLP down projection
     (500, 777, 513, "gemm_f32_direct_32x32x32_w4_buf", [400, 1, 1]),  # unaligned, <= half the CUs: buffer loads
 ])
 def test_gemm_launch_plans(m, n, k, kernel, grid):
-    # Grids of >= 256 tiles of 256x256 as 128x128 tiles, unless that grid's
+    # Persistent 128x128 tiles (gemm_ring.hip) for whole 128x128 tiles, K a
+    # multiple of 256 and at least 512, at least 256 tiles, in place of
+    # 128x128/256x256 plans or where ceil(t/256) <= t/256/0.9. Otherwise:
+    # grids of >= 256 tiles of 256x256 as 128x128 tiles, unless that grid's
     # last round would be under a quarter full: then 256x256 for the whole
     # rounds (the rest as 128x128, 128x64 or 64x64 tiles); else the best of
     # 128x128 / 128x64 / 64x64 by round fill x tile
@@ -301,8 +311,9 @@ def test_every_gemm_shape_routes_to_a_launch():
     # Long K (register-staged 64-bit loads) and operands of 2 GiB or more
     # with unaligned rows (clamped loads, two K groups at most).
     shapes += [(64, 64, 8912896), (1000, 777, 2097153), (300, 700, 2097153), (8192, 8192, 8)]
-    # 256x256 whole rounds with a 64x64 or 128x128 tail.
-    shapes += [(5120, 5120, 2048), (4352, 4096, 1024)]
+    # 256x256 whole rounds with a 64x64 or 128x128 tail (K not a multiple of
+    # 256), and the persistent kernel.
+    shapes += [(5120, 5120, 2080), (4352, 4096, 1056), (4096, 4096, 4096)]
     for m, n, k in shapes:
         d = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
         assert d["hip_supported"] and d["launch"]["kernel"], (m, n, k, d["hip_error"])
@@ -311,7 +322,7 @@ def test_every_gemm_shape_routes_to_a_launch():
                 "gemm_f32_direct_32x32x32_w4_buf", "gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x64x32",
                 "gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_k2", "gemm_f32_mfma_64x64x32_k4",
                 "gemm_f32_mfma_64x64x32_splitk_k2", "gemm_f32_direct_32x32x32_w4",
-                "gemm_f32_direct_32x32x32_w4_splitk"}
+                "gemm_f32_direct_32x32x32_w4_splitk", "gemm_f32_ring_128x128x32"}
     assert families <= seen, families - seen
 
 
