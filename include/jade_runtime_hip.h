@@ -127,6 +127,16 @@ int jr_fill_values(float *out, size_t len, uint32_t seed, float scale);
  * u2=(s>>8)/2^24, mean + sigma*sqrt(-2 ln u1)*cos(2 pi u2) in FP64. */
 int jr_fill_normal(float *out, size_t len, uint32_t seed, float mean, float sigma);
 
+/* No counterpart in the reference (introspection of jr_execute_dispatches):
+ * validates the batch exactly as jr_execute_dispatches does, enqueues
+ * nothing, and writes the launches it would make, in order, as
+ * space-separated "form:first_job" items, form one of single, pair
+ * (two GEMMs of one shape in one launch), gate_up_swiglu (gate and up GEMMs
+ * with their SwiGLU) or gemm_residual (a GEMM with the Add of its output).
+ * Codes as above (1 invalid, 2 runtime). */
+int jr_plan_dispatches(void *ctx, const jr_dispatch *jobs, size_t job_count, char *out, size_t out_cap, char *err,
+                       size_t cap);
+
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): C = A B for device pointers A [m,k], B [k,n], C [m,n]

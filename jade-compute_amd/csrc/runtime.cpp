@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "batch.hpp"
 #include "jade_runtime_hip.h"
 #include "kernels.hpp"
 #include "pipeline.hpp"
@@ -70,90 +71,34 @@ void emit(const std::string &text, char *out, size_t out_cap) {
     jade::dev::copy_text(text, out, out_cap);
 }
 
-// ---- batch planning for jr_execute_dispatches -----------------------------
+// ---- batches: checks and planning in batch.cpp, launches here --------------
 
-const KernelSpec &spec_of(const jr_dispatch &d) { return static_cast<Pipeline *>(d.kernel)->spec; }
+using jade::batch::Step;
 
-bool is_gemm(const KernelSpec &s) { return s.op == Op::Gemm || s.op == Op::GemmSimd; }
+// The context's pipelines and region table, as the batch unit sees them.
+class BatchView final : public jade::batch::Context {
+public:
+    explicit BatchView(RuntimeContext &c) : c_(c) {}
+    const KernelSpec *kernel(const void *handle) const override {
+        void *h = const_cast<void *>(handle);
+        return h && c_.pipelines.holds(h) ? &static_cast<Pipeline *>(h)->spec : nullptr;
+    }
+    bool region(const void *ptr, size_t &bytes, uint64_t &serial) const override {
+        const auto *r = c_.session.region(ptr);
+        if (!r) return false;
+        bytes = r->bytes;
+        serial = r->serial;
+        return true;
+    }
 
-// Two consecutive jobs run as one paired GEMM launch when both are GEMMs of
-// the same shape whose plan pairs, and neither touches the other's output:
-// job y must not read or write x's C (read-after-write, write-after-write) and
-// x must not read y's C (write-after-read). Each output is then bit-identical
-// to ordered launches.
-bool pairable(const jr_dispatch &x, const jr_dispatch &y) {
-    const KernelSpec &a = spec_of(x), &b = spec_of(y);
-    if (!is_gemm(a) || !is_gemm(b) || a.m != b.m || a.n != b.n || a.k != b.k) return false;
-    if (x.buffer_count != 3 || y.buffer_count != 3) return false;
-    if (!jade::hipk::gemm_f32_pairable(a.m, a.n, a.k)) return false;
-    for (int i = 0; i < 3; ++i)
-        if (y.buffers[i] == x.buffers[2] || x.buffers[i] == y.buffers[2]) return false;
-    return true;
-}
-
-bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-// Three consecutive jobs run as one fused launch when they are the residual
-// MLP's gate and up projections and their SwiGLU (src/runtime/workloads.rs:
-// 440-465): two pairable GEMMs on the same A, then swi_glu(x's C, y's C -> D)
-// over m*n elements, with D none of the GEMMs' inputs, a shape whose plan is
-// whole 128x64 tiles and 16-byte aligned inputs. The three outputs are
-// bit-identical to the ordered launches (gemm_f32_dual_swiglu).
-bool fusable_gate_up_swiglu(const jr_dispatch &x, const jr_dispatch &y, const jr_dispatch &z) {
-    if (!pairable(x, y) || z.buffer_count != 3) return false;
-    const KernelSpec &g = spec_of(x), &f = spec_of(z);
-    if (f.op != Op::SwiGlu || uint64_t(f.len) != uint64_t(g.m) * g.n) return false;
-    if (x.buffers[0] != y.buffers[0] || z.buffers[0] != x.buffers[2] || z.buffers[1] != y.buffers[2]) return false;
-    void *const d = z.buffers[2];
-    if (d == x.buffers[0] || d == x.buffers[1] || d == y.buffers[1]) return false;
-    return aligned16(x.buffers[0]) && aligned16(x.buffers[1]) && aligned16(y.buffers[1]) &&
-           jade::hipk::gemm_f32_dual_swiglu_fits(g.m, g.n, g.k);
-}
-
-// A GEMM and the Add that follows it run as one launch when the GEMM's output
-// P is one operand of the Add (add(P, X -> O) or add(X, P -> O) over m*n
-// elements), X is not P, and O is neither of the GEMM's inputs (the epilogue
-// writes O while other workgroups still read them): the residual MLP's down
-// projection and residual add (src/runtime/workloads.rs:440-465). P and O are
-// bit-identical to the ordered launches (gemm_f32_residual).
-bool fusable_gemm_residual(const jr_dispatch &x, const jr_dispatch &y) {
-    const KernelSpec &g = spec_of(x), &a = spec_of(y);
-    if (!is_gemm(g) || a.op != Op::Add || x.buffer_count != 3 || y.buffer_count != 3) return false;
-    if (uint64_t(a.len) != uint64_t(g.m) * g.n) return false;
-    void *const p = x.buffers[2];
-    if (y.buffers[0] != p && y.buffers[1] != p) return false;
-    void *const residual = y.buffers[0] == p ? y.buffers[1] : y.buffers[0];
-    void *const o = y.buffers[2];
-    if (residual == p || o == x.buffers[0] || o == x.buffers[1]) return false;
-    return aligned16(x.buffers[0]) && aligned16(x.buffers[1]) && jade::hipk::gemm_f32_residual_fits(g.m, g.n, g.k);
-}
-
-// One launch of the batch: job `first` alone, or it and the one or two jobs
-// after it as one paired or fused launch.
-struct Step {
-    enum class Form { Single, Pair, GateUpSwiglu, GemmResidual } form;
-    size_t first;
+private:
+    RuntimeContext &c_;
 };
 
-std::vector<Step> plan_steps(const jr_dispatch *jobs, size_t n) {
-    std::vector<Step> steps;
-    for (size_t j = 0; j < n;) {
-        if (j + 2 < n && fusable_gate_up_swiglu(jobs[j], jobs[j + 1], jobs[j + 2])) {
-            steps.push_back({Step::Form::GateUpSwiglu, j});
-            j += 3;
-        } else if (j + 1 < n && pairable(jobs[j], jobs[j + 1])) {
-            steps.push_back({Step::Form::Pair, j});
-            j += 2;
-        } else if (j + 1 < n && fusable_gemm_residual(jobs[j], jobs[j + 1])) {
-            steps.push_back({Step::Form::GemmResidual, j});
-            j += 2;
-        } else {
-            steps.push_back({Step::Form::Single, j});
-            j += 1;
-        }
-    }
-    return steps;
-}
+const jade::batch::LaunchRules kLaunchRules{jade::hipk::gemm_f32_pairable, jade::hipk::gemm_f32_dual_swiglu_fits,
+                                            jade::hipk::gemm_f32_residual_fits};
+
+const KernelSpec &spec_of(const jr_dispatch &d) { return static_cast<Pipeline *>(d.kernel)->spec; }
 
 hipError_t run_step(const Step &step, const jr_dispatch *jobs, hipStream_t q) {
     const jr_dispatch &x = jobs[step.first];
@@ -184,12 +129,6 @@ hipError_t run_step(const Step &step, const jr_dispatch *jobs, hipStream_t q) {
         }
     }
     return hipErrorInvalidValue;
-}
-
-void check_batch(const void *jobs, size_t job_count, uint32_t repeats, const double *gpu_ms) {
-    if (!jobs || !job_count) refuse_invalid("the batch holds no jobs");
-    if (!repeats) refuse_invalid("repeats must be at least 1");
-    if (!gpu_ms) refuse_invalid("no place to write the measured milliseconds");
 }
 
 }  // namespace
@@ -262,7 +201,7 @@ extern "C" int jr_execute(void *handle, const jr_job *jobs, size_t job_count, ui
                           char *err, size_t cap) {
     if (gpu_ms) *gpu_ms = 0;
     return entry(err, cap, [&] {
-        check_batch(jobs, job_count, repeats, gpu_ms);
+        jade::batch::check_batch(jobs, job_count, repeats, gpu_ms);
         for (size_t j = 0; j < job_count; ++j) {
             if (!jobs[j].launch) refuse_invalid(text_of("job %zu has no launcher", j));
             if (!jobs[j].buffers || !jobs[j].buffer_count) refuse_invalid(text_of("job %zu binds no buffers", j));
@@ -328,31 +267,12 @@ extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size
                                      double *gpu_ms, char *err, size_t cap) {
     if (gpu_ms) *gpu_ms = 0;
     return entry(err, cap, [&] {
-        check_batch(jobs, job_count, repeats, gpu_ms);
+        jade::batch::check_batch(jobs, job_count, repeats, gpu_ms);
         RuntimeContext &c = context_of(handle);
-        // The whole batch is checked before anything is enqueued
-        // (corex.rs:556-569): owned kernel, owned regions, binding count,
-        // exact lengths, no write aliasing.
-        std::vector<uint64_t> lengths, ids;
-        for (size_t j = 0; j < job_count; ++j) {
-            const std::string where = text_of("job %zu", j);
-            const Pipeline &p = pipeline_of(c, jobs[j].kernel, where.c_str());
-            if (!jobs[j].buffers && jobs[j].buffer_count) refuse_invalid(where + ": null buffer list");
-            lengths.assign(jobs[j].buffer_count, 0);
-            ids.assign(jobs[j].buffer_count, 0);
-            for (size_t b = 0; b < jobs[j].buffer_count; ++b) {
-                const auto *r = c.session.region(jobs[j].buffers[b]);
-                if (!r) refuse_invalid(text_of("job %zu: buffer %zu is not a live region of this context", j, b));
-                if (r->bytes % sizeof(float))
-                    refuse_invalid(text_of("job %zu: buffer %zu is not a whole number of f32 elements", j, b));
-                lengths[b] = r->bytes / sizeof(float);
-                ids[b] = r->serial;
-            }
-            std::string error;
-            if (!jade::validate_bindings(p.spec, lengths.data(), ids.data(), jobs[j].buffer_count, error))
-                refuse_invalid(where + ": " + error);
-        }
-        const std::vector<Step> steps = plan_steps(jobs, job_count);
+        const BatchView view(c);
+        // The whole batch is checked before anything is enqueued.
+        jade::batch::validate(jobs, job_count, view);
+        const std::vector<Step> steps = jade::batch::plan_steps(jobs, job_count, view, kLaunchRules);
         c.session.make_current();
         *gpu_ms = c.session.clocked(repeats, [&](hipStream_t q) -> hipError_t {
             for (const Step &s : steps) {
@@ -361,5 +281,24 @@ extern "C" int jr_execute_dispatches(void *handle, const jr_dispatch *jobs, size
             }
             return hipSuccess;
         });
+    });
+}
+
+extern "C" int jr_plan_dispatches(void *handle, const jr_dispatch *jobs, size_t job_count, char *out, size_t out_cap,
+                                  char *err, size_t cap) {
+    if (out && out_cap) out[0] = '\0';
+    return entry(err, cap, [&] {
+        if (!out || !out_cap) refuse_invalid("jr_plan_dispatches needs an output buffer");
+        double unused = 0;
+        jade::batch::check_batch(jobs, job_count, 1, &unused);
+        RuntimeContext &c = context_of(handle);
+        const BatchView view(c);
+        jade::batch::validate(jobs, job_count, view);
+        std::string text;
+        for (const Step &s : jade::batch::plan_steps(jobs, job_count, view, kLaunchRules)) {
+            static const char *const forms[] = {"single", "pair", "gate_up_swiglu", "gemm_residual"};
+            text += text_of("%s%s:%zu", text.empty() ? "" : " ", forms[int(s.form)], s.first);
+        }
+        emit(text, out, out_cap);
     });
 }

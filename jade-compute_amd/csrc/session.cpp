@@ -5,42 +5,17 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <string>
 #include <vector>
 
 namespace jade {
 namespace dev {
-
-std::string text_of(const char *format, ...) {
-    va_list args;
-    va_start(args, format);
-    va_list again;
-    va_copy(again, args);
-    const int n = std::vsnprintf(nullptr, 0, format, args);
-    va_end(args);
-    std::string out;
-    if (n > 0) {
-        out.resize(size_t(n) + 1);
-        std::vsnprintf(&out[0], out.size(), format, again);
-        out.resize(size_t(n));
-    }
-    va_end(again);
-    return out;
-}
-
-void refuse(Kind kind, std::string text) { throw Refusal{kind, std::move(text)}; }
 
 void expect(hipError_t status, const char *step) {
     if (status == hipSuccess) return;
     const Kind kind = status == hipErrorOutOfMemory ? Kind::Memory : Kind::Device;
     refuse(kind, text_of("%s failed with %s (HIP status %d: %s)", step, hipGetErrorName(status), int(status),
                          hipGetErrorString(status)));
-}
-
-void copy_text(const std::string &text, char *out, size_t cap) {
-    if (!out || !cap) return;
-    const size_t n = text.size() < cap - 1 ? text.size() : cap - 1;
-    std::memcpy(out, text.data(), n);
-    out[n] = '\0';
 }
 
 Session::Session(int ordinal) {
@@ -165,7 +140,15 @@ std::string Session::device_summary() const {
     int runtime = 0, driver = 0;
     expect(hipRuntimeGetVersion(&runtime), "reading the HIP runtime version");
     expect(hipDriverGetVersion(&driver), "reading the driver version");
-    return text_of("hip:%d %s isa=%s cus=%d hbm_bytes=%llu hip_runtime=%d hip_driver=%d", ordinal_, prop.name,
+    // The reference's info names the device (native/jade_runtime_corex.cpp:
+    // 88-89). Some drivers report no product name; the ISA name (without its
+    // feature suffixes) stands in for it then.
+    std::string name(prop.name);
+    if (name.find_first_not_of(" \t") == std::string::npos) {
+        name = prop.gcnArchName;
+        name = name.substr(0, name.find(':'));
+    }
+    return text_of("hip:%d name=%s isa=%s cus=%d hbm_bytes=%llu hip_runtime=%d hip_driver=%d", ordinal_, name.c_str(),
                    prop.gcnArchName, prop.multiProcessorCount, static_cast<unsigned long long>(prop.totalGlobalMem),
                    runtime, driver);
 }

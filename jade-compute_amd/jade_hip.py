@@ -81,6 +81,7 @@ def load(path: Optional[str] = None) -> ctypes.CDLL:
         "jr_kernel_describe": (_c.c_int, [_vp, _vp, _cp, _sz, _cp, _sz]),
         "jr_execute_dispatches": (_c.c_int, [_vp, _c.POINTER(_Dispatch), _sz, _c.c_uint32,
                                              _c.POINTER(_c.c_double), _cp, _sz]),
+        "jr_plan_dispatches": (_c.c_int, [_vp, _c.POINTER(_Dispatch), _sz, _cp, _sz, _cp, _sz]),
         "jr_buffer_elements": (_c.c_int, [_vp, _vp, _c.POINTER(_sz), _cp, _sz]),
         "jr_fill_values": (_c.c_int, [_vp, _sz, _c.c_uint32, _c.c_float]),
         "jr_fill_normal": (_c.c_int, [_vp, _sz, _c.c_uint32, _c.c_float, _c.c_float]),
@@ -291,10 +292,7 @@ class HipRuntime:
         _check(self._lib.jr_kernel_describe(self._ctx, handle.value, out, len(out), err, len(err)), err)
         return Kernel(self, handle.value, json.loads(out.value.decode()))
 
-    def execute(self, jobs: Sequence, repeats: int) -> Execution:
-        """jobs: sequence of (Kernel, [Buffer, ...]) in dispatch order."""
-        if not jobs or repeats <= 0:
-            raise JadeError(1, "execution requires jobs and positive repeats")
+    def _dispatches(self, jobs: Sequence):
         arrays = []
         native = (_Dispatch * len(jobs))()
         for i, (kernel, buffers) in enumerate(jobs):
@@ -307,6 +305,25 @@ class HipRuntime:
             native[i].kernel = kernel.handle
             native[i].buffers = _c.cast(ptrs, _c.POINTER(_vp))
             native[i].buffer_count = len(buffers)
+        return native, arrays
+
+    def plan(self, jobs: Sequence) -> list:
+        """The launches execute() would make for these jobs, as (form, first
+        job) pairs: form "single", "pair", "gate_up_swiglu" or
+        "gemm_residual" (jr_plan_dispatches)."""
+        if not jobs:
+            raise JadeError(1, "a plan needs jobs")
+        native, _keep = self._dispatches(jobs)
+        out = _c.create_string_buffer(1 << 16)
+        err = _error_buffer()
+        _check(self._lib.jr_plan_dispatches(self._ctx, native, len(jobs), out, len(out), err, len(err)), err)
+        return [(form, int(first)) for form, first in (item.split(":") for item in out.value.decode().split())]
+
+    def execute(self, jobs: Sequence, repeats: int) -> Execution:
+        """jobs: sequence of (Kernel, [Buffer, ...]) in dispatch order."""
+        if not jobs or repeats <= 0:
+            raise JadeError(1, "execution requires jobs and positive repeats")
+        native, _keep = self._dispatches(jobs)
         gpu_ms = _c.c_double(0.0)
         err = _error_buffer()
         started = time.perf_counter()

@@ -341,7 +341,10 @@ def manifest(folder, rt, steps):
         commit = subprocess.check_output(["git", "rev-parse", "HEAD"], cwd=ROOT, text=True,
                                          stderr=subprocess.DEVNULL).strip()
     except (OSError, subprocess.CalledProcessError):
-        commit = None  # the GPU box gets a snapshot without .git
+        # A snapshot without .git (the GPU box): the commit build() recorded
+        # next to the library it built ("<sha> dirty" when the tree differed).
+        recorded = ROOT / "jade-compute_amd" / "build_commit.txt"
+        commit = recorded.read_text().strip() if recorded.is_file() else None
     library = jade_hip.LIBRARY_PATH
     return {"schema_version": SCHEMA_VERSION, "source_commit": commit,
             "source_files": {str(p.relative_to(ROOT)): sha(p) for p in sources if p.is_file()},

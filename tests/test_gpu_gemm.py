@@ -392,13 +392,16 @@ def test_gemm_plan_abi_bench_flow():
         plan.close()
 
 
-def _gemm_batch(runtime, jobs_spec, arrays, repeats=1):
-    # jobs_spec: list of (m, n, k, [names of A, B, C]); arrays: name -> host array or element count
+def _gemm_batch(runtime, jobs_spec, arrays, repeats=1, launches=None):
+    # jobs_spec: list of (m, n, k, [names of A, B, C]); arrays: name -> host array or element count;
+    # launches: the launch plan the batch must take (jr_plan_dispatches).
     bufs = {}
     for name, value in arrays.items():
         bufs[name] = runtime.resident(value) if isinstance(value, np.ndarray) else runtime.alloc(value)
     jobs = [(runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}), [bufs[x] for x in names])
             for m, n, k, names in jobs_spec]
+    if launches is not None:
+        assert runtime.plan(jobs) == launches, runtime.plan(jobs)
     runtime.execute(jobs, repeats)
     out = {name: runtime.download(buf) for name, buf in bufs.items()}
     for buf in bufs.values():
@@ -408,16 +411,19 @@ def _gemm_batch(runtime, jobs_spec, arrays, repeats=1):
 
 def test_paired_gemms_match_separate_launches(runtime):
     # Two independent GEMMs of one shape (the MLP's gate and up projections)
-    # run as one paired launch; each output must equal its own launch bit for bit.
-    m = n = k = 1024
+    # run as one paired launch (a shape whose plan is one-group 128x64 tiles;
+    # K-group, split, direct and persistent plans do not pair); each output
+    # must equal its own launch bit for bit.
+    m, n, k = 2048, 2048, 1056
     a, b0, b1 = orc.values(m * k, 0x31, 1.0), orc.values(k * n, 0x32, 1.0), orc.values(k * n, 0x33, 1.0)
     both = _gemm_batch(runtime, [(m, n, k, ["a", "b0", "c0"]), (m, n, k, ["a", "b1", "c1"])],
-                       {"a": a, "b0": b0, "b1": b1, "c0": m * n, "c1": m * n})
+                       {"a": a, "b0": b0, "b1": b1, "c0": m * n, "c1": m * n}, launches=[("pair", 0)])
     one = _gemm_batch(runtime, [(m, n, k, ["a", "b0", "c0"])], {"a": a, "b0": b0, "c0": m * n})
     two = _gemm_batch(runtime, [(m, n, k, ["a", "b1", "c1"])], {"a": a, "b1": b1, "c1": m * n})
     np.testing.assert_array_equal(both["c0"], one["c0"])
     np.testing.assert_array_equal(both["c1"], two["c1"])
-    gate(both["c1"], m, n, k, a, b1)
+    gate(both["c1"], m, n, k, a, b1, rows=(0, 256))
+    gate(both["c0"], m, n, k, a, b0, rows=(m - 256, m))
 
 
 def test_dependent_gemms_keep_order(runtime):
@@ -426,7 +432,7 @@ def test_dependent_gemms_keep_order(runtime):
     m = n = k = 1024
     a, b = orc.values(m * k, 0x41, 1.0), orc.values(k * n, 0x42, 0.03)
     raw = _gemm_batch(runtime, [(m, n, k, ["a", "b", "c0"]), (m, n, k, ["c0", "b", "c1"])],
-                      {"a": a, "b": b, "c0": m * n, "c1": m * n})
+                      {"a": a, "b": b, "c0": m * n, "c1": m * n}, launches=[("single", 0), ("single", 1)])
     c0 = orc.gemm_reference(m, n, k, a, b).astype(np.float32)
     gate(raw["c0"], m, n, k, a, b)
     gate(raw["c1"], m, n, k, raw["c0"], b)

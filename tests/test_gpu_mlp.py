@@ -62,12 +62,15 @@ def test_config_c4_mlp(runtime):
     print(f"C4 MLP all {batch * width} outputs: max_abs {check.max_abs_error:.3e}", flush=True)
 
 
-def _run_jobs(runtime, specs, arrays, plan, repeats=1, one_at_a_time=False):
+def _run_jobs(runtime, specs, arrays, plan, repeats=1, one_at_a_time=False, launches=None):
     # specs: name -> spec; arrays: name -> host array or element count;
-    # plan: list of (spec name, [buffer names]).
+    # plan: list of (spec name, [buffer names]); launches: the launch plan
+    # the batch must take (jr_plan_dispatches), checked before it runs.
     kernels = {name: runtime.compile(spec) for name, spec in specs.items()}
     bufs = {name: runtime.resident(v) if isinstance(v, np.ndarray) else runtime.alloc(v) for name, v in arrays.items()}
     jobs = [(kernels[s], [bufs[b] for b in names]) for s, names in plan]
+    if launches is not None:
+        assert runtime.plan(jobs) == launches, runtime.plan(jobs)
     if one_at_a_time:
         for _ in range(repeats):
             for job in jobs:
@@ -95,7 +98,7 @@ def test_fused_gate_up_swiglu_is_bit_identical(runtime, m, n, k):
     arrays = {"x": orc.normal(m * k, 0x21), "wg": orc.normal(k * n, 0x22, 0.0, 0.1),
               "wu": orc.normal(k * n, 0x23, 0.0, 0.1), "g": m * n, "u": m * n, "d": m * n}
     plan = [("gemm", ["x", "wg", "g"]), ("gemm", ["x", "wu", "u"]), ("swiglu", ["g", "u", "d"])]
-    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2, launches=[("gate_up_swiglu", 0)])
     alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
     for name in ("g", "u", "d"):
         np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
@@ -119,7 +122,7 @@ def test_swiglu_writing_a_gemm_input_is_not_fused(runtime):
     arrays = {"x": orc.normal(m * k, 0x31, 0.0, 0.05), "wg": orc.normal(k * n, 0x32, 0.0, 0.05),
               "wu": orc.normal(k * n, 0x33, 0.0, 0.05), "g": m * n, "u": m * n}
     plan = [("gemm", ["x", "wg", "g"]), ("gemm", ["x", "wu", "u"]), ("swiglu", ["g", "u", "wg"])]
-    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2, launches=[("single", 0), ("single", 1), ("single", 2)])
     ordered = _run_jobs(runtime, specs, arrays, plan, repeats=2, one_at_a_time=True)
     for name in ("g", "u", "wg"):
         np.testing.assert_array_equal(batched[name], ordered[name], err_msg=name)
@@ -142,7 +145,7 @@ def test_fused_gemm_residual_is_bit_identical(runtime, m, n, k, order):
               "x": orc.normal(m * n, 0x43), "p": m * n, "o": m * n}
     operands = ["p", "x"] if order == "px" else ["x", "p"]
     plan = [("gemm", ["a", "w", "p"]), ("add", operands + ["o"])]
-    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2, launches=[("gemm_residual", 0)])
     alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
     for name in ("p", "o"):
         np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
@@ -161,7 +164,7 @@ def test_add_writing_a_gemm_input_is_not_fused(runtime):
     arrays = {"a": orc.normal(m * k, 0x51, 0.0, 0.05), "w": orc.normal(k * n, 0x52, 0.0, 0.05),
               "x": orc.normal(m * n, 0x53, 0.0, 0.05), "p": m * n}
     plan = [("gemm", ["a", "w", "p"]), ("add", ["p", "x", "a"])]
-    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    batched = _run_jobs(runtime, specs, arrays, plan, repeats=2, launches=[("single", 0), ("single", 1)])
     ordered = _run_jobs(runtime, specs, arrays, plan, repeats=2, one_at_a_time=True)
     for name in ("a", "p"):
         np.testing.assert_array_equal(batched[name], ordered[name], err_msg=name)
@@ -185,7 +188,8 @@ def test_c4_block_fused_equals_ordered_launches(runtime):
     plan = [("norm", ["x", "gamma", "normalized"]), ("up", ["normalized", "wg", "gate"]),
             ("up", ["normalized", "wu", "upv"]), ("swiglu", ["gate", "upv", "act"]), ("down", ["act", "wd", "proj"]),
             ("add", ["proj", "x", "out"])]
-    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2)
+    fused = _run_jobs(runtime, specs, arrays, plan, repeats=2,
+                      launches=[("single", 0), ("gate_up_swiglu", 1), ("gemm_residual", 4)])
     alone = _run_jobs(runtime, specs, arrays, plan, one_at_a_time=True)
     for name in ("normalized", "gate", "upv", "act", "proj", "out"):
         np.testing.assert_array_equal(fused[name], alone[name], err_msg=name)
