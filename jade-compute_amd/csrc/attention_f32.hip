@@ -65,6 +65,12 @@ __device__ inline float halves_sum(float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// NB adjacent floats of one LDS row, read as one vector (NB = 1, 2 or 4).
+template <int NB>
+struct alignas(4 * NB) VRow {
+    float x[NB];
+};
+
 template <int DP, int NW>
 struct AttnShape {
     static constexpr int kThreads = NW * 64;
@@ -193,7 +199,10 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
     constexpr int LD = S::kLD;
     __shared__ float lds[2 * 2 * S::kTile];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // The wave index through readfirstlane: the compiler then knows every
+    // per-wave condition below (causal sub-tiles, unmasked tiles) is uniform
+    // and branches on scalars.
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
     const int h = lane >> 5, c = lane & 31;
     auto tiles_of = [&](int b) { return ((CAUSAL ? min(seq, b * S::kBQ + S::kBQ) : seq) + kBKV - 1) / kBKV; };
     int head = int(blockIdx.x), qb = int(gridDim.y) - 1 - int(blockIdx.y);  // longest causal rows first
@@ -239,9 +248,11 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
         }
     }
 
-    f32x16 acc[DP / 32];
+    constexpr int NB = DP / 32;  // accumulator blocks of O^T
+    constexpr bool kInterleaved = NB == 4;  // block b holds dims NB r + b (else 32 b + r)
+    f32x16 acc[NB];
 #pragma unroll
-    for (int b = 0; b < DP / 32; ++b)
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[b][v] = 0.f;
     float row_max = -INFINITY, row_sum = 0.f;
@@ -403,20 +414,35 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
             // lane and the rescale is the identity: skip it (wave-uniform).
             if (__any(old_weight != 1.0f)) {
 #pragma unroll
-                for (int b = 0; b < DP / 32; ++b) acc[b] *= old_weight;
+                for (int b = 0; b < NB; ++b) acc[b] *= old_weight;
             }
 
-            // O^T += V^T P^T over the live sub-tiles.
+            // O^T += V^T P^T over the live sub-tiles. At head dim 128 the dims
+            // are interleaved over the four accumulator blocks (block b, row r
+            // holds dim 4r + b), so a lane's V operands of one key step for all
+            // blocks are four adjacent floats, one ds_read_b128 where blocks
+            // of 32 dims took four reads: LLM config 132.0 -> 133.9 TFLOP/s,
+            // H64 S2048 D128 noncausal 135.1 -> 137.6. At head dim 64 (two
+            // blocks, ds_read_b64) it was 1.5% slower, so there block b keeps
+            // dims [32b, 32b + 32).
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb) {
                 if (sb < subs) {
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int key = sb * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                        const float *vrow = vs + key * LD + c;
+                        if constexpr (kInterleaved) {
+                            const VRow<NB> vr = *reinterpret_cast<const VRow<NB> *>(vs + key * LD + NB * c);
 #pragma unroll
-                        for (int b = 0; b < DP / 32; ++b)
-                            acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[sb][v], acc[b], 0, 0, 0);
+                            for (int b = 0; b < NB; ++b)
+                                acc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr.x[b], st[sb][v], acc[b], 0, 0, 0);
+                        } else {
+                            const float *vrow = vs + key * LD + c;
+#pragma unroll
+                            for (int b = 0; b < NB; ++b)
+                                acc[b] =
+                                    __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * b], st[sb][v], acc[b], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -441,21 +467,40 @@ __global__ __launch_bounds__(NW * 64) void attention_online_mfma(const float *__
             orow += z * rows * size_t(dim);
             inv = 1.0f;
         }
+        if constexpr (kInterleaved) {
+            // Register v of block b holds dim 4 (8 (v >> 2) + 4h + (v & 3)) + b:
+            // for each v the four blocks give four adjacent dims.
 #pragma unroll
-        for (int b = 0; b < DP / 32; ++b) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int d = 32 * b + 8 * g + 4 * h;
+            for (int v = 0; v < 16; ++v) {
+                const int d = NB * (8 * (v >> 2) + 4 * h + (v & 3));
                 if (VEC) {
                     if (d < dim) {
-                        const f32x4 out = {acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv, acc[b][4 * g + 2] * inv,
-                                           acc[b][4 * g + 3] * inv};
+                        const f32x4 out = {acc[0][v] * inv, acc[1][v] * inv, acc[2][v] * inv, acc[3][v] * inv};
                         *reinterpret_cast<f32x4 *>(orow + d) = out;
                     }
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (d + e < dim) orow[d + e] = acc[b][4 * g + e] * inv;
+                    for (int b = 0; b < NB; ++b)
+                        if (d + b < dim) orow[d + b] = acc[b][v] * inv;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * b + 8 * g + 4 * h;
+                    if (VEC) {
+                        if (d < dim) {
+                            const f32x4 out = {acc[b][4 * g] * inv, acc[b][4 * g + 1] * inv, acc[b][4 * g + 2] * inv,
+                                               acc[b][4 * g + 3] * inv};
+                            *reinterpret_cast<f32x4 *>(orow + d) = out;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (d + e < dim) orow[d + e] = acc[b][4 * g + e] * inv;
+                    }
                 }
             }
         }
