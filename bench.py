@@ -357,11 +357,23 @@ def bench_copy(rt, steps, warmup):
     return out
 
 
+FLOOR_QUEUED = 4000   # near-empty launches queued behind the long ones
+FLOOR_LONG = 10       # 4096^3 GEMMs ahead of them (about 9 ms of device work)
+
+
 def bench_floor(rt, steps, warmup):
-    """Per-launch time of near-empty launches back to back on the runtime's
-    stream: the dispatch floor under every short kernel (one workgroup copying
-    64 floats; 256 workgroups adding 262144 floats, 1 MiB per operand)."""
+    """Per-launch time of near-empty launches on the runtime's stream (one
+    workgroup copying 64 floats; 256 workgroups adding 262144 floats, 1 MiB
+    per operand), two ways:
+    - back to back as the host enqueues them (jr_execute_dispatches replaying
+      the one job): the host's enqueue rate bounds it;
+    - behind a full queue: FLOOR_QUEUED of them enqueued after FLOOR_LONG
+      4096^3 GEMMs in one batch, so all are queued before the device reaches
+      them; the time over the GEMMs alone, per launch, is the device-side
+      cost of a launch. Median of SAMPLES interleaved pairs of batches."""
     out = {}
+    long_p = prepare_gemm(rt, 4096, 4096, 4096)
+    long_job = long_p.workload.jobs[0]
     for name, spec, n in (("copy_64", {"op": "elementwise", "len": 64, "inputs": 1,
                                         "expression": {"kind": "input", "binding": 0}}, 64),
                           ("add_256_workgroups", {"op": "add", "len": 262144}, 262144)):
@@ -369,10 +381,20 @@ def bench_floor(rt, steps, warmup):
         count = spec.get("inputs", 2)
         bufs = [rt.resident(jade_hip.fill_values(n, 0x77 + i, 1.0)) for i in range(count)] + [rt.alloc(n)]
         t = measure({name: Workload(rt, [(kernel, bufs)])}, steps, warmup)[name]
+        job = (kernel, bufs)
+        rt.execute([long_job] * FLOOR_LONG + [job] * FLOOR_QUEUED, 1)  # warm-up
+        alone, behind = [], []
+        for _ in range(SAMPLES):
+            alone.append(rt.execute([long_job] * FLOOR_LONG, 1).gpu_ms)
+            behind.append(rt.execute([long_job] * FLOOR_LONG + [job] * FLOOR_QUEUED, 1).gpu_ms)
+        per = [1e3 * (b - a) / FLOOR_QUEUED for a, b in zip(alone, behind)]
         out[name] = {"us_per_launch": 1e3 * t["ms_per_step"], "min_us": 1e3 * t["min_ms_per_step"],
-                     "launch": kernel.launch}
+                     "behind_full_queue_us": 1e3 * (median(behind) - median(alone)) / FLOOR_QUEUED,
+                     "behind_full_queue_range_us": [min(per), max(per)],
+                     "queued": FLOOR_QUEUED, "long_launches": FLOOR_LONG, "launch": kernel.launch}
         for b in bufs:
             b.free()
+    long_p.close()
     return out
 
 
@@ -691,6 +713,9 @@ def main():
         extra["copy_calibration"] = bench_copy(rt, K, W)
     if wl == "floor":  # launch-floor measurement only; not part of the default line
         extra["launch_floor"] = bench_floor(rt, max(K, 200), W)
+        for name, f in extra["launch_floor"].items():
+            log(f"  floor {name}: {f['us_per_launch']:.2f} us back to back, "
+                f"{f['behind_full_queue_us']:.2f} us behind a full queue")
     if wl == "mfma":  # counter runs only; not part of the default line
         extra["mfma_shapes"] = bench_mfma_shapes(rt, K, W)
     if wl in ("all", "sweep"):
