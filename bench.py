@@ -138,9 +138,20 @@ def measure(workloads, steps, warmup, min_repeats=SAMPLE_REPEATS):
     return {name: workloads[name].summary() for name in names}
 
 
-def traffic_from_profiles(symbol_prefix, launch):
-    """HBM bytes per launch of this kernel at this grid, from the committed
-    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/traffic.json), or None."""
+def symbol_of(launch_kernel):
+    """The kernel symbol prefix (as rocprofv3 names it) of a launch that
+    jr_kernel_describe reports as `launch_kernel`."""
+    for prefix in ("gemm_f32_ring", "gemm_f32_mfma_256", "gemm_f32_direct", "gemm_f32_dual_swiglu",
+                   "attention_online_mfma", "attention_pairs_mfma"):
+        if launch_kernel.startswith(prefix):
+            return prefix
+    return "gemm_f32_mfma"
+
+
+def traffic_from_profiles(symbol_prefix, launch, workload):
+    """HBM bytes per launch of this kernel at this grid in the counter run of
+    `workload` (bench.py --workload ...), from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (profiles/traffic.json), or None."""
     path = os.path.join(PROFILE_DIR, "traffic.json")
     if not os.path.exists(path):
         return None
@@ -150,11 +161,11 @@ def traffic_from_profiles(symbol_prefix, launch):
         table = json.load(open(path))
     except (OSError, ValueError):
         return None
-    # Keys are "symbol@work-items@workgroup"; one symbol prefix can name
-    # several instantiations, so an ambiguous match gives no figure.
+    # Keys are "symbol@work-items@workgroup@workload"; one symbol prefix can
+    # name several instantiations, so an ambiguous match gives no figure.
     found = [entry.get("bytes_per_launch") for key, entry in table.items()
-             if len(key.split("@")) == 3 and key.split("@")[0].startswith(symbol_prefix)
-             and key.split("@")[1:] == [str(items), str(block)]]
+             if len(key.split("@")) == 4 and key.split("@")[0].startswith(symbol_prefix)
+             and key.split("@")[1:] == [str(items), str(block), workload]]
     return found[0] if len(found) == 1 else None
 
 
@@ -307,8 +318,10 @@ def bench_mlp(rt, batch, width, hidden, steps, warmup):
         if name in gemm_flops:
             t = measure({name: Workload(rt, [job])}, steps, warmup)[name]
             ms = t["ms_per_step"]
+            spec = dict(specs)[name]
             per[name] = {"ms": ms, "tflops": gemm_flops[name] / (ms * 1e-3) / 1e12,
-                         "frac_mfma": gemm_flops[name] / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS}
+                         "frac_mfma": gemm_flops[name] / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS,
+                         "kernel": job[0].launch["kernel"], "shape": f"{spec['m']}x{spec['n']}x{spec['k']}"}
     total_flops = sum(gemm_flops.values())
     for buf in (xg, ng, wgg, wug, wdg, normalized, gate, up, act, proj, out):
         buf.free()
@@ -423,34 +436,97 @@ def _short(name):
     return name.split("(")[0] if "(" in name else name
 
 
-def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
+def _workload_of(path):
+    """The workload a counter file belongs to: the name of the directory that
+    holds the rocprofv3 output of one `bench.py --workload ...` run."""
+    return os.path.basename(os.path.dirname(path))
+
+
+def bench_gemm_launches(bench_log):
+    """(shape, launch kernel name, event-timed ms per launch) of every GEMM
+    that a bench.py JSON line in `bench_log` reports: the headline, the MLP's
+    GEMMs launched alone and the sweep."""
+    line = None
+    with open(bench_log, errors="replace") as f:
+        for text in f:
+            if text.startswith('{"metric"'):
+                line = json.loads(text)
+    if line is None:
+        return []
+    out = []
+    head = line.get("gpu_kernel", {})
+    if "m" in head:
+        out.append((f"{head['m']}x{head['n']}x{head['k']}", head["kernel"], head["ms_per_step"]))
+    extra = line.get("extra", {})
+    for name, op in extra.get("mlp_4096x1024x2816", {}).get("per_op", {}).items():
+        if "shape" in op:
+            out.append((op["shape"], op["kernel"], op["ms"]))
+    for shape, r in extra.get("gemm_sweep", {}).items():
+        out.append((shape, r["kernel"], r["ms"]))
+    return out
+
+
+def split_by_shape(durations_ns, launches, tolerance=0.25):
+    """Dispatches of one kernel symbol that serves several shapes at one grid
+    (the persistent GEMM), assigned to the shape whose event-timed median is
+    nearest in log scale; a dispatch further than `tolerance` from every
+    median (warm-up at low clocks, pre-heat) stays unassigned. Returns
+    {shape or None: [durations]}."""
+    groups = {}
+    medians = {}
+    for shape, _, ms in launches:
+        medians.setdefault(shape, ms * 1e6)
+    for d in durations_ns:
+        best = min(medians, key=lambda sh: abs(np.log(d / medians[sh])))
+        label = best if abs(d / medians[best] - 1.0) <= tolerance else None
+        groups.setdefault(label, []).append(d)
+    return groups
+
+
+def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None, bench_log=None):
     """Per (kernel, grid) durations from a rocprofv3 --kernel-trace run, plus HBM
-    bytes per launch from --pmc FETCH_SIZE and WRITE_SIZE runs, scaled by what the
-    same counters read for the copy kernel of known size (COPY_ELEMENTS)."""
+    bytes per launch from --pmc FETCH_SIZE and WRITE_SIZE runs (one output
+    directory per bench.py workload, rows kept apart by workload), scaled by
+    what the same counters read for the copy kernel of known size
+    (COPY_ELEMENTS). With `bench_log` (the profiled run's output), dispatches
+    of the persistent GEMM, whose grid is the same at every shape, are split
+    by shape against the bench's own event-timed medians."""
     trace = _read_csv(_find(trace_dir, "kernel_trace.csv"))
     groups = {}
     for row in trace:
         key = (_short(row["Kernel_Name"]), int(row["Grid_Size_X"]), int(row["Grid_Size_Y"]),
                int(row["Grid_Size_Z"]), int(row["Workgroup_Size_X"]))
         groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    launches = bench_gemm_launches(bench_log) if bench_log else []
+    ring_shapes = [x for x in launches if x[1].startswith("gemm_f32_ring")]
+    rows = []
+    for key, durations in groups.items():
+        if key[0].startswith("gemm_f32_ring") and ring_shapes:
+            for shape, part in split_by_shape(durations, ring_shapes).items():
+                rows.append((key[0] + (f" [{shape}]" if shape else " [unassigned]"), key[1:], part))
+        else:
+            rows.append((key[0], key[1:], durations))
     counters = {}
     for directory, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
         if not directory:
             continue
-        # One counter_collection.csv per profiled run; a directory may hold
-        # several runs (one per workload).
+        # One counter_collection.csv per profiled run, in a directory named
+        # for its workload; a directory may hold several runs.
         for path in _find_all(directory, "counter_collection.csv"):
             for row in _read_csv(path):
                 if row.get("Counter_Name") != counter:
                     continue
-                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]))
+                key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]),
+                       _workload_of(path))
                 counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
     lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us |",
              "|---|---|---|---|---|---|---|"]
-    for key, durations in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
-        name, gx, gy, gz, wg = key
+    for name, (gx, gy, gz, wg), durations in sorted(rows, key=lambda r: -sum(r[2])):
         lines.append(f"| {name} | {gx}x{gy}x{gz} | {wg} | {len(durations)} | {np.mean(durations) / 1e3:.2f} | "
                      f"{np.min(durations) / 1e3:.2f} | {np.max(durations) / 1e3:.2f} |")
+    if ring_shapes:
+        lines += ["", "Event-timed medians of the same run (bench.py's own figures, ms per launch): " +
+                  ", ".join(f"{shape} {ms * 1e3:.2f} us ({kernel})" for shape, kernel, ms in launches)]
     traffic = {}
     if counters:
         copy_key = next((k for k in counters if k[0] == "copy_stream"), None)
@@ -461,30 +537,33 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None):
             scale[counter] = expected_kib / measured if measured and np.isfinite(measured) else np.nan
         lines += ["", f"HBM counter calibration (copy_stream, {COPY_ELEMENTS * 4 / 2**20:.0f} MiB in and out): "
                       f"scale FETCH_SIZE x{scale['FETCH_SIZE']:.4f}, WRITE_SIZE x{scale['WRITE_SIZE']:.4f}", "",
-                  "| kernel | grid (work-items) | block | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | scaled MB/launch |",
-                  "|---|---|---|---|---|---|---|"]
+                  "| kernel | workload | grid (work-items) | block | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB "
+                  "| scaled MB/launch |",
+                  "|---|---|---|---|---|---|---|---|"]
         for key, vals in sorted(counters.items()):
             fetch = np.mean(vals.get("FETCH_SIZE", [np.nan]))
             write = np.mean(vals.get("WRITE_SIZE", [np.nan]))
             nbytes = (fetch * scale["FETCH_SIZE"] + write * scale["WRITE_SIZE"]) * 1024.0
             count = max(len(vals.get("FETCH_SIZE", [])), len(vals.get("WRITE_SIZE", [])))
-            lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {count} | {fetch:.0f} | {write:.0f} | "
+            if key[0].startswith("__amd_rocclr"):
+                continue
+            lines.append(f"| {key[0]} | {key[3]} | {key[1]} | {key[2]} | {count} | {fetch:.0f} | {write:.0f} | "
                          f"{nbytes / 1e6:.1f} |")
             if np.isfinite(nbytes):
-                traffic[f"{key[0]}@{key[1]}@{key[2]}"] = {"bytes_per_launch": nbytes, "fetch_kib": fetch,
-                                                          "write_kib": write}
+                traffic[f"{key[0]}@{key[1]}@{key[2]}@{key[3]}"] = {"bytes_per_launch": nbytes, "fetch_kib": fetch,
+                                                                   "write_kib": write}
     return "\n".join(lines), traffic
 
 
 # Shapes for MFMA-utilisation counter runs: each launch keeps the summed
 # SQ_VALU_MFMA_BUSY_CYCLES below the 2^31 at which the counter saturates, and
-# each exercises one production kernel (128x128 and 128x64 GEMM tiles, 64x64
-# tiles with four K groups, direct-load 32x32 tiles, the 256x256 tile with a
-# 64x64 tail, unaligned rows on 64x64 tiles with two K groups, the MLP's down
-# projection with its residual epilogue shape, direct-load tiles split over K;
-# the split-key, four-wave and eight-wave attention launches).
-MFMA_GEMMS = ((4096, 4096, 2048), (2048, 2048, 2048), (1024, 1024, 1024), (512, 512, 512), (5120, 5120, 1024),
-              (1000, 777, 513), (4096, 1024, 2816), (16, 1024, 2816))
+# each exercises one production kernel (64x64 tiles with four K groups,
+# direct-load 32x32 tiles, unaligned rows on 64x64 tiles with two K groups,
+# direct-load tiles split over K; the eight-wave paired, four-wave and
+# eight-wave online attention launches). The persistent GEMM launches one grid
+# at every shape, so its counter rows cannot be told apart within one run:
+# its shapes are counted one per run (--workload shape).
+MFMA_GEMMS = ((1024, 1024, 1024), (512, 512, 512), (1000, 777, 513), (16, 1024, 2816))
 MFMA_ATTENTION = ((8, 1024, 64, False), (8, 1024, 64, True), (32, 2048, 64, True), (64, 2048, 128, True))
 SIMDS = 1024  # 256 CUs x 4 SIMDs
 XCDS = 8
@@ -503,17 +582,19 @@ def bench_mfma_shapes(rt, steps, warmup):
 
 
 def summarize_mfma(directory):
-    """MFMA busy share per (kernel, grid) from a rocprofv3 --pmc run with
-    SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: busy / (GUI cycles per XCD x
-    SIMDs). GRBM_GUI_ACTIVE is summed over the 8 XCDs."""
+    """MFMA busy share per (kernel, grid, workload) from rocprofv3 --pmc runs
+    with SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, one output directory per
+    bench.py workload: busy / (GUI cycles per XCD x SIMDs). GRBM_GUI_ACTIVE is
+    summed over the 8 XCDs."""
     vals = {}
     for path in _find_all(directory, "counter_collection.csv"):
         for row in _read_csv(path):
-            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]))
+            key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]),
+                   _workload_of(path))
             vals.setdefault(key, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
-    lines = ["| kernel | grid (work-items) | block | dispatches | GRBM_GUI_ACTIVE / XCD | SQ_VALU_MFMA_BUSY_CYCLES "
-             "| MFMA busy |",
-             "|---|---|---|---|---|---|---|"]
+    lines = ["| kernel | workload | grid (work-items) | block | dispatches | GRBM_GUI_ACTIVE / XCD "
+             "| SQ_VALU_MFMA_BUSY_CYCLES | MFMA busy |",
+             "|---|---|---|---|---|---|---|---|"]
     for key, v in sorted(vals.items()):
         if "SQ_VALU_MFMA_BUSY_CYCLES" not in v or "GRBM_GUI_ACTIVE" not in v:
             continue
@@ -522,8 +603,8 @@ def summarize_mfma(directory):
         if busy <= 0:
             continue
         flag = " (saturated)" if busy >= 2.0 ** 31 else ""
-        lines.append(f"| {key[0]} | {key[1]} | {key[2]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | {busy:.4g}{flag} | "
-                     f"{100.0 * busy / (gui * SIMDS):.1f}% |")
+        lines.append(f"| {key[0]} | {key[3]} | {key[1]} | {key[2]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | "
+                     f"{busy:.4g}{flag} | {100.0 * busy / (gui * SIMDS):.1f}% |")
     return "\n".join(lines)
 
 
@@ -630,13 +711,18 @@ def main():
     ap.add_argument("--preheat-ms", type=float, default=PREHEAT_MS,
                     help="untimed device time of each workload before its samples (0 for counter runs)")
     ap.add_argument("--workload", default="all",
-                    choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma", "floor"])
+                    choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma", "floor",
+                             "shape"])
+    ap.add_argument("--shape", default="4096x4096x2048", metavar="MxNxK",
+                    help="the one GEMM of --workload shape (counter runs of one shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--summarize-rocprof", metavar="TRACE_DIR",
                     help="print per-kernel tables from a rocprofv3 --kernel-trace output directory and exit")
     ap.add_argument("--pmc-fetch", metavar="DIR", help="rocprofv3 --pmc FETCH_SIZE output directory")
     ap.add_argument("--pmc-write", metavar="DIR", help="rocprofv3 --pmc WRITE_SIZE output directory")
-    ap.add_argument("--traffic-out", metavar="JSON", help="write HBM bytes per launch per (kernel, grid)")
+    ap.add_argument("--traffic-out", metavar="JSON", help="write HBM bytes per launch per (kernel, grid, workload)")
+    ap.add_argument("--bench-log", metavar="FILE",
+                    help="output of the profiled bench.py run: splits the persistent GEMM's trace rows by shape")
     ap.add_argument("--summarize-mfma", metavar="PMC_DIR",
                     help="print MFMA busy shares from a rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE "
                          "output directory and exit")
@@ -652,7 +738,7 @@ def main():
         print(summarize_mfma(args.summarize_mfma))
         return
     if args.summarize_rocprof:
-        table, traffic = summarize_rocprof(args.summarize_rocprof, args.pmc_fetch, args.pmc_write)
+        table, traffic = summarize_rocprof(args.summarize_rocprof, args.pmc_fetch, args.pmc_write, args.bench_log)
         print(table)
         if args.traffic_out:
             with open(args.traffic_out, "w") as f:
@@ -718,6 +804,12 @@ def main():
                 f"{f['behind_full_queue_us']:.2f} us behind a full queue")
     if wl == "mfma":  # counter runs only; not part of the default line
         extra["mfma_shapes"] = bench_mfma_shapes(rt, K, W)
+    if wl == "shape":  # one GEMM shape (counter runs); not part of the default line
+        m, n, k = (int(x) for x in args.shape.split("x"))
+        r = bench_gemm(rt, m, n, k, K, W)
+        extra["gemm_shape"] = {"shape": args.shape, "ms": r["ms_per_step"], "tflops": r["tflops"],
+                               "kernel": r["kernel"], "launch": r["launch"]}
+        log(f"  {args.shape} {r['tflops']:.1f} TFLOP/s ({r['kernel']})")
     if wl in ("all", "sweep"):
         sweep = {}
         for m, n, k in ((512, 512, 512), (1024, 1024, 1024), (2048, 2048, 2048), (1000, 777, 513),
@@ -738,7 +830,7 @@ def main():
         config = {"workload": "FP32 GEMM C=A.B 4096x4096x4096, row-major (BASELINE configs[1] headline)",
                   "m": 4096, "n": 4096, "k": 4096,
                   "inputs": "validation::inputs xorshift32 seeds 0x12345678/0x9abcdef1, U[-1,1)"}
-        symbol = "gemm_f32_mfma"
+        symbol = symbol_of(gemm["launch"]["kernel"])
     else:
         config = {"workload": "FP32 causal attention B4 H32 S4096 D128 (BASELINE configs[4])"}
         symbol = "attention_online_mfma"
@@ -765,13 +857,13 @@ def main():
         "preheat_ms": head["preheat_ms"],
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": achieved / PEAK_FP32_MFMA_TFLOPS,
-                     "traffic": traffic_from_profiles(symbol, head["launch"])},
+                     "traffic": traffic_from_profiles(symbol, head["launch"], "gemm" if gemm else "attention")},
     }
     if attention is not None and gemm is not None:
         att = {k: v for k, v in attention.items() if not k.startswith("_")}
         att["roofline"] = {"bound": "mfma", "achieved": attention["tflops"], "peak": PEAK_FP32_MFMA_TFLOPS,
                            "unit": "TFLOP/s", "frac": attention["tflops"] / PEAK_FP32_MFMA_TFLOPS,
-                           "traffic": traffic_from_profiles("attention_online_mfma", attention["launch"])}
+                           "traffic": traffic_from_profiles("attention_online_mfma", attention["launch"], "attention")}
         line["attention"] = att
     if not args.no_cpu_baseline and gemm is not None:
         log("cpu baseline ...")

@@ -1,7 +1,8 @@
 """bench.py's harness on the CPU: its rocprofv3 summaries on synthetic
 profiler CSVs (the HBM counter calibration against the copy kernel, the
-per-(kernel, grid, workgroup) traffic table, the lookup that fills the bench
-line's `roofline.traffic`) and the time-based pre-heat on a stand-in runtime."""
+per-(kernel, grid, workgroup, workload) traffic table, the lookup that fills
+the bench line's `roofline.traffic`, the split of one symbol's trace rows by
+shape) and the time-based pre-heat on a stand-in runtime."""
 import csv
 import importlib.util
 import os
@@ -58,11 +59,12 @@ def make_profile(bench, tmp_path):
 def test_traffic_table_is_keyed_by_workgroup_and_calibrated(bench, tmp_path):
     text, traffic = make_profile(bench, tmp_path)
     assert "scale FETCH_SIZE x2.0000, WRITE_SIZE x1.0000" in text
-    assert set(traffic) == {"copy_stream@16777216@256", "gemm_f32_mfma<2, 2, true, 1, 1>@262144@256",
-                            "gemm_f32_mfma<1, 1, true, 1, 4>@262144@1024"}
-    assert traffic["gemm_f32_mfma<2, 2, true, 1, 1>@262144@256"]["bytes_per_launch"] == pytest.approx(
+    # Keys carry the workload: the name of the directory of the counter run.
+    assert set(traffic) == {"copy_stream@16777216@256@w", "gemm_f32_mfma<2, 2, true, 1, 1>@262144@256@w",
+                            "gemm_f32_mfma<1, 1, true, 1, 4>@262144@1024@w"}
+    assert traffic["gemm_f32_mfma<2, 2, true, 1, 1>@262144@256@w"]["bytes_per_launch"] == pytest.approx(
         (1000.0 * 2 + 500.0) * 1024)
-    assert traffic["copy_stream@16777216@256"]["bytes_per_launch"] == pytest.approx(2 * bench.COPY_ELEMENTS * 4)
+    assert traffic["copy_stream@16777216@256@w"]["bytes_per_launch"] == pytest.approx(2 * bench.COPY_ELEMENTS * 4)
 
 
 def test_traffic_lookup_picks_the_launched_instantiation(bench, tmp_path, monkeypatch):
@@ -72,14 +74,38 @@ def test_traffic_lookup_picks_the_launched_instantiation(bench, tmp_path, monkey
     (tmp_path / "profiles").mkdir()
     (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(traffic))
     monkeypatch.setattr(bench, "PROFILE_DIR", str(tmp_path / "profiles"))
-    big = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]})
-    small = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [256, 1, 1], "block": [1024, 1, 1]})
+    big = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}, "w")
+    small = bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [256, 1, 1], "block": [1024, 1, 1]}, "w")
     assert big == pytest.approx(2500.0 * 1024) and small == pytest.approx(250.0 * 1024)
-    # No entry, or a prefix that names two instantiations of one launch shape: no figure.
-    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [7, 1, 1], "block": [256, 1, 1]}) is None
-    traffic["gemm_f32_mfma<9, 9, true, 1, 1>@262144@256"] = {"bytes_per_launch": 1.0}
+    # Another workload's run, no entry, or a prefix that names two
+    # instantiations of one launch shape: no figure.
+    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}, "x") is None
+    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [7, 1, 1], "block": [256, 1, 1]}, "w") is None
+    traffic["gemm_f32_mfma<9, 9, true, 1, 1>@262144@256@w"] = {"bytes_per_launch": 1.0}
     (tmp_path / "profiles" / "traffic.json").write_text(json.dumps(traffic))
-    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}) is None
+    assert bench.traffic_from_profiles("gemm_f32_mfma", {"grid": [1024, 1, 1], "block": [256, 1, 1]}, "w") is None
+
+
+def test_persistent_gemm_rows_split_by_shape(bench, tmp_path):
+    # One symbol at one grid for three shapes: each dispatch goes to the shape
+    # whose event-timed median is nearest, or stays unassigned beyond 25%.
+    ring = SYMBOL.format("gemm_f32_ring<1, true>")
+    durations_us = [935, 940, 2540, 120, 125, 180, 3300]
+    trace = [{"Kernel_Name": ring, "Grid_Size_X": 256, "Grid_Size_Y": 1, "Grid_Size_Z": 1, "Workgroup_Size_X": 512,
+              "Start_Timestamp": 0, "End_Timestamp": int(d * 1000)} for d in durations_us]
+    write_csv(str(tmp_path / "trace" / "run_kernel_trace.csv"), trace)
+    line = {"metric": "m", "gpu_kernel": {"m": 4096, "n": 4096, "k": 4096, "kernel": "gemm_f32_ring_128x128x32",
+                                          "ms_per_step": 0.936},
+            "extra": {"gemm_sweep": {"2048x2048x2048": {"ms": 0.122, "kernel": "gemm_f32_ring_128x128x32"},
+                                     "4096x11008x4096": {"ms": 2.54, "kernel": "gemm_f32_ring_128x128x32"},
+                                     "512x512x512": {"ms": 0.0064, "kernel": "gemm_f32_direct_32x32x32_w4"}}}}
+    log = tmp_path / "bench.log"
+    log.write_text("device: test\n" + __import__("json").dumps(line) + "\n")
+    text, _ = bench.summarize_rocprof(str(tmp_path / "trace"), bench_log=str(log))
+    rows = {ln.split("|")[1].strip(): ln.split("|")[4].strip() for ln in text.splitlines()
+            if ln.startswith("| gemm_f32_ring")}
+    assert rows == {"gemm_f32_ring<1, true> [4096x4096x4096]": "2", "gemm_f32_ring<1, true> [4096x11008x4096]": "1",
+                    "gemm_f32_ring<1, true> [2048x2048x2048]": "2", "gemm_f32_ring<1, true> [unassigned]": "2"}
 
 
 def test_preheat_follows_the_command_line_value(bench, monkeypatch):
