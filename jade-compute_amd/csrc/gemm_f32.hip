@@ -322,8 +322,8 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // barrier publishes the stage and retires the buffer the next loads overwrite.
 // The matrix cores sum kFoldStages stages into `part` before each fold into
 // acc (four against two: 4096^3 139.0 -> 141.1 TFLOP/s, 2048^3 131.8 ->
-// 133.9; the worst 4096^3 output then uses 20% of the 1e-4 tolerance against
-// 17.5%). `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
+// 133.9; the worst 4096^3 output then used 20% of the 1e-4 tolerance against
+// 17.5%; eight timed the same as four here). `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
 // group (every group of a workgroup runs the same number of stages, so the
 // barriers match).
 template <int TM, int TN, bool BUF = false>
@@ -1003,8 +1003,9 @@ __device__ inline void issue_stage(const float *__restrict__ A, const float *__r
 }
 
 // One (64 TM) x 64 tile at (m0, n0): its gate product in waves 0-3, its up
-// product in waves 4-7.
-template <int TM>
+// product in waves 4-7. FOLD: stages per run before each fold, that of the
+// kernel each product would run on alone.
+template <int TM, int FOLD>
 __device__ inline void tile(const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu,
                             float *__restrict__ G, float *__restrict__ U, float *__restrict__ Act, int N, int K,
                             int m0, int n0, float *smem) {
@@ -1025,12 +1026,12 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
     issue_stage<TM>(A, B, N, K, m0, n0, 0, lds0, wave, lane);
     drain_vmem();
     __syncthreads();
-    // The LDS-direct loop's schedule: partial sums over kFoldStages stages,
-    // then a fold.
+    // The LDS-direct loop's schedule: partial sums over FOLD stages, then a
+    // fold.
     f32x16 part[TM][1];
-    for (int kt = 0; kt < nk; kt += kFoldStages) {
+    for (int kt = 0; kt < nk; kt += FOLD) {
 #pragma unroll
-        for (int uu = 0; uu < kFoldStages; ++uu) {
+        for (int uu = 0; uu < FOLD; ++uu) {
             const int k = kt + uu, u = uu & 1;
             if (k < nk) {
                 const float *cur = smem + u * S::kStage;
@@ -1042,7 +1043,7 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
                     mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
                 else
                     mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
-                if (uu == kFoldStages - 1 || k + 1 == nk) {
+                if (uu == FOLD - 1 || k + 1 == nk) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
                 }
@@ -1083,6 +1084,7 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
 // Workgroups [0, tiles_m body_tn) take the 128x64 tiles of columns
 // [0, 64 body_tn) in the XCD-grouped order; the rest take the 64x64 tiles of
 // the columns right of them, row-major.
+template <int FOLD>
 __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
     const float *__restrict__ A, const float *__restrict__ Bg, const float *__restrict__ Bu, float *__restrict__ G,
     float *__restrict__ U, float *__restrict__ Act, int N, int K, int tiles_m, int tiles_n, int body_tn) {
@@ -1092,10 +1094,10 @@ __global__ __launch_bounds__(dual::kThreads) void gemm_f32_dual_swiglu(
         const int pos = xcd_order(int(blockIdx.x), body);
         int tm, tn;
         grouped_tile(pos, tiles_m, body_tn, tm, tn);
-        dual::tile<2>(A, Bg, Bu, G, U, Act, N, K, tm * 128, tn * 64, smem);
+        dual::tile<2, FOLD>(A, Bg, Bu, G, U, Act, N, K, tm * 128, tn * 64, smem);
     } else {
         const int pos = int(blockIdx.x) - body, edge_n = tiles_n - body_tn;
-        dual::tile<1>(A, Bg, Bu, G, U, Act, N, K, (pos / edge_n) * 64, (body_tn + pos % edge_n) * 64, smem);
+        dual::tile<1, FOLD>(A, Bg, Bu, G, U, Act, N, K, (pos / edge_n) * 64, (body_tn + pos % edge_n) * 64, smem);
     }
 }
 
@@ -1981,7 +1983,8 @@ hipError_t gemm_f32_residual(hipStream_t stream, const float *a, const float *b,
 bool gemm_f32_dual_swiglu_fits(uint32_t m, uint32_t n, uint32_t k) {
     // The plan each product would take alone must give the fused kernel's
     // bits: the 128x64 tile (paired), or the persistent kernel, whose outputs
-    // take the same MFMA steps over k and the same folds per output.
+    // take the same MFMA steps over k; the fused launch then folds as that
+    // plan does (every kFoldStages or ring::kFoldRun stages).
     const Route r = route_for(m, n, k);
     const Plan &p = r.plan;
     const bool same_bits = r.launchable && (p.ring || (gemm_f32_pairable(m, n, k) && p.tm == 2 && p.tn == 1));
@@ -2009,8 +2012,12 @@ hipError_t gemm_f32_dual_swiglu(hipStream_t stream, const float *a, const float 
     const int tiles_m = int(m / dual::T::kBM), tiles_n = int(n / dual::T::kBN);
     const int edge_n = dual_edge_columns(tiles_m, tiles_n), body_tn = tiles_n - edge_n;
     const unsigned grid = unsigned(tiles_m * body_tn + 2 * tiles_m * edge_n);
-    hipLaunchKernelGGL(gemm_f32_dual_swiglu, dim3(grid), dim3(dual::kThreads), 0, stream, a, bg, bu, g, u, act,
-                       int(n), int(k), tiles_m, tiles_n, body_tn);
+    if (route_for(m, n, k).plan.ring)
+        hipLaunchKernelGGL(gemm_f32_dual_swiglu<ring::kFoldRun>, dim3(grid), dim3(dual::kThreads), 0, stream, a, bg,
+                           bu, g, u, act, int(n), int(k), tiles_m, tiles_n, body_tn);
+    else
+        hipLaunchKernelGGL(gemm_f32_dual_swiglu<kFoldStages>, dim3(grid), dim3(dual::kThreads), 0, stream, a, bg,
+                           bu, g, u, act, int(n), int(k), tiles_m, tiles_n, body_tn);
     return hipGetLastError();
 }
 

@@ -38,11 +38,13 @@ namespace {
 //    they re-read the last tile into a slot nothing reads), the load cursor
 //    advances by selects, and each tile's first iteration, which stores the
 //    previous tile, is a separate instantiation of the eight-stage body.
-// Accumulation is the LDS-direct loops' two-level scheme, with their run
-// length and MFMA order, so outputs are bit-identical to the 128x128 tile
-// kernel: runs of kFoldStages stages sum in MFMA accumulators and are folded
-// into the running sums with VALU adds. The fold of a block sits right before
-// that block's first MFMA of the next run.
+// Accumulation is the LDS-direct loops' two-level scheme with their MFMA
+// order and a longer run: runs of kFoldRun (eight) stages sum in MFMA
+// accumulators and are folded into the running sums with VALU adds, where the
+// tile loops fold every four stages. The fold of a block sits right before
+// that block's first MFMA of the next run. The fused gate/up kernel takes the
+// same run length where it stands in for this kernel, so its outputs stay
+// bit-identical to this kernel's.
 //
 // Measured at 4096^3 (TFLOP/s, A/B on one box; the non-persistent 128x128
 // kernel ran 141.6): first form, four waves of 64x64 with all of a stage's
@@ -51,13 +53,15 @@ namespace {
 // instructions per stage), 145.7; operand reads interleaved with the MFMAs
 // instead of issued back to back (the waves then waited on the LDS pipe four
 // times as long as the library's kernel), 147.4 with four waves and 149.3 with
-// eight. Folding every eight stages instead of four added 0.5% and was not
-// taken: it raises the worst output's share of the 1e-4 tolerance.
+// eight; runs of eight stages instead of four before each fold (kFoldRun),
+// 149.4. Halving the barriers (a timing-only copy without the odd stages'
+// barriers) and folding the two waves of a SIMD at different stages (so one
+// wave's MFMAs cover the other's fold) were measured and changed nothing.
 // Requires M, N multiples of 128, K a multiple of 256 (whole eight-stage
 // iterations per tile), 16-byte aligned operands, 32-bit load offsets.
 namespace ring_local {
 using namespace ring;
-static_assert(kUnroll % kFoldStages == 0 && kUnroll % kDepth == 0, "slot and run start are compile-time per stage");
+static_assert(kUnroll % kFoldRun == 0 && kUnroll % kDepth == 0, "slot and run start are compile-time per stage");
 
 // One quarter of a stage's operands for one lane: a[i] = A[row block i][k
 // 16h + 4q + e] at a[i][e]; b[e] = B[k 16h + 4q + e][columns 2c, 2c + 1].
@@ -262,7 +266,7 @@ __global__ __launch_bounds__(512 / TM) __attribute__((amdgpu_waves_per_eu(3 - TM
         constexpr int U = decltype(uc)::value;
         constexpr bool FIRST = decltype(fc)::value;
         constexpr int slot = U % kDepth;
-        constexpr bool run_start = U % kFoldStages == 0;
+        constexpr bool run_start = U % kFoldRun == 0;
         wait_loads_barrier<(FIRST && U == 1) ? 0 : kLoads>();  // publishes stage g + 1
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

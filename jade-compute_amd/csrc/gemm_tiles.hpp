@@ -16,6 +16,12 @@ constexpr int kBM = 128, kBN = 128;
 constexpr int kDepth = 4;   // 32-deep stages resident in LDS
 constexpr int kUnroll = 8;  // stages per loop iteration; K must be a multiple of 32 * kUnroll
 constexpr int kThreads = 512;  // eight waves of 32x64
+// Stages summed in MFMA accumulators before each fold: eight, where the tile
+// loops fold every four. Against four: 4096^3 928 -> 920 us (+0.8%),
+// 4096x11008x4096 2648 -> 2620, 4096x1024x2816 164.4 -> 162.9; the worst
+// 4096^3 output then uses a third of the 1e-4 + 1e-4|e| tolerance (a fifth
+// with four).
+constexpr int kFoldRun = 8;
 constexpr uint32_t kAStageB = kBM * 32 * 4, kBStageB = 32 * kBN * 4;  // 16 KiB each
 constexpr uint32_t kBRegion = kDepth * kAStageB;                      // B stages from 64 KiB
 constexpr uint32_t kLdsBytes = kDepth * (kAStageB + kBStageB);        // 128 KiB
@@ -34,9 +40,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kBK = 32;
-// Stages whose products the LDS-direct loops (and the fused gate/up kernel,
-// which must match them bit for bit) sum in MFMA accumulators before each
-// fold into the running sums: 4 stages, 128 k.
+// Stages whose products the LDS-direct tile loops (and the fused gate/up
+// kernel where it stands in for them, which must match them bit for bit) sum
+// in MFMA accumulators before each fold into the running sums: 4 stages,
+// 128 k. Eight measured 0.5-18% slower on these loops (6144x1024x1024 103.5
+// -> 122 us, 3072^3 499 -> 505, 1024x1024x4096 73.2 -> 74.5); the persistent
+// kernel folds every ring::kFoldRun stages.
 constexpr int kFoldStages = 4;
 constexpr int kGroupM = 8;
 
