@@ -78,7 +78,7 @@ class Workload:
 
     def __init__(self, rt, jobs, launches=1):
         self.rt, self.jobs, self.launches = rt, jobs, launches
-        self.preheat_ms = 0.0
+        self.preheat_ms, self.preheat_steps = 0.0, 0
         self.samples, self.sizes, self.host = [], [], []
 
     def warm(self, warmup):
@@ -93,7 +93,16 @@ class Workload:
         while self.preheat_ms < target_ms:
             ex = self.rt.execute(self.jobs, batch)
             self.preheat_ms += ex.gpu_ms or 0.0
+            self.preheat_steps += batch
             batch = min(2 * batch, 1 << 14)
+
+    def min_sample_steps(self):
+        """Steps that make a sample last at least MIN_SAMPLE_MS of device time,
+        from the pre-heat's per-step time (1 without a pre-heat)."""
+        if self.preheat_steps == 0 or self.preheat_ms <= 0.0:
+            return 1
+        per_step = self.preheat_ms / self.preheat_steps
+        return min(MAX_SAMPLE_STEPS, int(np.ceil(MIN_SAMPLE_MS / per_step)))
 
     def sample(self, steps):
         ex = self.rt.execute(self.jobs, steps)
@@ -115,8 +124,14 @@ class Workload:
 
 
 # Steps per sample outside the headline: the reference's ten repeats per
-# sample (reports/METAL_ADVANCES.md:109-112), or more when `steps` asks.
+# sample (reports/METAL_ADVANCES.md:109-112), or more when `steps` asks, and
+# enough that a sample runs at least MIN_SAMPLE_MS of device time. A sample is
+# one jr_execute_dispatches call: its first launch starts on an idle queue and
+# pays the dispatch latency once, which ten launches of a few microseconds
+# would carry as a third of a microsecond each.
 SAMPLE_REPEATS = 10
+MIN_SAMPLE_MS = 1.0
+MAX_SAMPLE_STEPS = 4096
 
 
 def measure(workloads, steps, warmup, min_repeats=SAMPLE_REPEATS):
@@ -124,7 +139,8 @@ def measure(workloads, steps, warmup, min_repeats=SAMPLE_REPEATS):
     sample round r runs the workloads in an order rotated by r
     (metal_lab.rs:179-187). The samples split `steps` evenly, each holding at
     least `min_repeats` steps (1 for the headline, which times exactly
-    `steps`). Returns {name: summary}."""
+    `steps`); outside the headline a workload's samples also hold enough steps
+    for MIN_SAMPLE_MS of device time. Returns {name: summary}."""
     names = list(workloads)
     for name in names:
         workloads[name].warm(warmup)
@@ -132,9 +148,11 @@ def measure(workloads, steps, warmup, min_repeats=SAMPLE_REPEATS):
     sizes = [max(size, min_repeats) for size in split_steps(steps)]
     if len(sizes) < SAMPLES and min_repeats > 1:
         sizes += [min_repeats] * (SAMPLES - len(sizes))
+    floor = {name: workloads[name].min_sample_steps() if min_repeats > 1 else 1 for name in names}
     for r, size in enumerate(sizes):
         for off in range(len(names)):
-            workloads[names[(r + off) % len(names)]].sample(size)
+            name = names[(r + off) % len(names)]
+            workloads[name].sample(max(size, floor[name]))
     return {name: workloads[name].summary() for name in names}
 
 

@@ -1436,6 +1436,213 @@ void launch_direct_g(hipStream_t stream, dim3 grid, bool bufa, const float *a, c
         launch_direct_gc<G, false>(stream, grid, bufa, bufb, a, b, c, m, n, k, lda, tiles_m, tiles_n, sa, sb, sc);
 }
 
+// ---- Direct tiles staged through LDS ----------------------------------------
+// The unsplit direct plan (32x32 tiles, wave g of G summing the K slices g,
+// g + G, ...) for aligned rows, one workgroup per CU: each wave moves its
+// slices into its own LDS region with 16-byte buffer loads into LDS (A 32x32
+// and B 32x32 per slice, 8 KiB), up to four slices ahead in a ring of at most
+// four slots, and reads its MFMA operands from there. The loads of a wave's
+// first slices all go out at entry as one-KiB requests; the register-staged
+// form issued 20 narrower loads per slice (B as single floats, one column per
+// lane) and its slices arrived a memory round trip apart. No barrier: a wave
+// reads only what its own loads wrote, counted by vmcnt.
+// Every wave runs S = ceil(slices / G) slices, fully unrolled: a wave with
+// one slice fewer runs a last slice of zeros (its loads aim past both
+// buffers, which reads zero without touching memory), so slots, LDS offsets
+// and wait counts are compile-time and the loop has no branch. Adding zero
+// products leaves the sums' bits unchanged (a chain that starts at +0 never
+// holds -0), and per output the MFMA steps, the chain and the reduction are
+// the register-staged kernel's: the outputs are bit-identical to it.
+// Measured at 512^3 (back to back, us): register-staged 5.87-6.14; this form
+// with a run-time slice loop 5.53, with branches on the slice count 5.18,
+// branch-free 4.78. Timestamps per wave (medians): the first slice consumed
+// 1.76 -> 1.44 us after entry, the other three 2.24 -> 1.36 us (their 48
+// MFMAs take 1.28 us at the peak rate).
+// A slot: A rows of 128 bytes, chunk j of row r at j ^ swz_a(r) (as the tile
+// kernels' A stages); then B rows of 128 bytes, row r in row slot
+// r ^ ((r >> 4) & 1), so that rows s and 16 + s, which one B operand read
+// takes for the two halves of the wave, sit on different banks.
+namespace dlds {
+constexpr uint32_t kSlotB = 8192;
+constexpr int kLoads = 8;       // one-KiB loads per slice: four of A, four of B
+constexpr int kMaxSlices = 6;   // per wave: direct::kChainSlices
+__host__ __device__ constexpr int ring(int s) { return s < 4 ? s : 4; }
+}  // namespace dlds
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    static_assert(N >= 0 && N <= 24 && N % 8 == 0, "wait counts of whole slices");
+    if constexpr (N == 0)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if constexpr (N == 8)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if constexpr (N == 16)
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+}
+
+template <int G, int S, bool WHOLE>
+__global__ __launch_bounds__(64 * G) void gemm_f32_direct_lds(const float *__restrict__ A,
+                                                              const float *__restrict__ B, float *__restrict__ C,
+                                                              int M, int N, int K, int tiles_m, int tiles_n) {
+    using namespace dlds;
+    static_assert(S >= 1 && S <= kMaxSlices, "slices per wave");
+    constexpr int kRing = ring(S);
+    constexpr uint32_t kWaveB = kRing * kSlotB;
+    __shared__ __attribute__((aligned(1024))) char lds[G * kWaveB];
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(A), 0, int(uint32_t(M) * uint32_t(K) * 4u), int(kBufferWord3));
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(B), 0, int(uint32_t(K) * uint32_t(N) * 4u), int(kBufferWord3));
+    int tm, tn;
+    tile_coords(tiles_m, tiles_n, tm, tn);
+    const int lane = threadIdx.x & 63;
+    const int g = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+    const int c = lane & 31, h = lane >> 5;
+    const int slices = (K + kBK - 1) / kBK;
+    char *region = lds + g * kWaveB;
+    // Per-lane byte offsets of the four A and four B loads of a slice at k 0;
+    // slice k0 adds 4 k0 (A) and 4 k0 N (B). Rows past M (and, through 32-bit
+    // wrap, far past it) read zero or rows that feed only unstored outputs;
+    // B runs past N read the next row's first columns, also unstored.
+    uint32_t aoff[4], boff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3), lc = (lane & 7) ^ swz_a(r);
+        aoff[i] = (uint32_t(tm * 32 + r) * uint32_t(K) + uint32_t(4 * lc)) * 4u;
+        const int p = 8 * i + (lane >> 3), row = p ^ ((p >> 4) & 1);
+        boff[i] = (uint32_t(row) * uint32_t(N) + uint32_t(tn * 32 + 4 * (lane & 7))) * 4u;
+    }
+    // Slice j of this wave into `slot`; a slice past K aims its loads past
+    // both buffers.
+    auto issue = [&](int j, int slot) {
+        const int sl = g + j * G;
+        const bool live = sl < slices;
+        const uint32_t k0 = uint32_t(sl) * kBK;
+        char *dst = region + slot * kSlotB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                ra, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16,
+                int(live ? aoff[i] + 4u * k0 : direct::kDeadOffset), 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rb, (__attribute__((address_space(3))) void *)(dst + 4096 + i * 1024), 16,
+                int(live ? boff[i] + 4u * k0 * uint32_t(N) : direct::kDeadOffset), 0, 0, 0);
+    };
+#pragma unroll
+    for (int j = 0; j < kRing; ++j) issue(j, j);
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+    auto slice = [&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int later = S - 1 - j < 3 ? S - 1 - j : 3;  // slices in flight behind this one
+        wait_vmcnt<kLoads * later>();
+        const char *sa = region + (j % kRing) * kSlotB;
+        const char *sb = sa + 4096;
+        f32x4 a[4];
+        float b[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            a[q] = *reinterpret_cast<const f32x4 *>(sa + c * 128 + (((4 * h + q) ^ swz_a(c)) << 4));
+#pragma unroll
+        for (int x = 0; x < 16; ++x) b[x] = *reinterpret_cast<const float *>(sb + ((16 * h + x) ^ h) * 128 + c * 4);
+        // Elements past K (the last slice of a ragged K): A is zeroed; B's rows
+        // past K lie past its buffer and read zero. One MFMA chain over all of
+        // the wave's slices, as the register-staged kernel runs the unsplit
+        // plans.
+        const int valid = K - (g + j * G) * kBK - 16 * h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int i = 4 * q + e;
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(WHOLE || i < valid ? a[q][e] : 0.f, b[i], acc, 0, 0, 0);
+            }
+        if constexpr (j + kRing < S) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue(j + kRing, j % kRing);  // the slot's operands are in registers
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    slice(std::integral_constant<int, 0>{});
+    if constexpr (S > 1) slice(std::integral_constant<int, 1>{});
+    if constexpr (S > 2) slice(std::integral_constant<int, 2>{});
+    if constexpr (S > 3) slice(std::integral_constant<int, 3>{});
+    if constexpr (S > 4) slice(std::integral_constant<int, 4>{});
+    if constexpr (S > 5) slice(std::integral_constant<int, 5>{});
+    // Every load has been waited for (the last slice waits for vmcnt 0): the
+    // G partial tiles meet in LDS (wave w's at the start of its region) and
+    // wave g then sums and stores entries v of its share, in wave order.
+    constexpr int kShare = 16 / G;
+    constexpr int kRegionF = int(kWaveB / 4);
+    float *red = reinterpret_cast<float *>(lds);
+    if (G > 1) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) red[g * kRegionF + v * 64 + lane] = acc[v];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kShare; ++j) {
+            const int v = g * kShare + j;
+            float total = red[v * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < G; ++w) total += red[w * kRegionF + v * 64 + lane];
+            acc[j] = total;
+        }
+    }
+    const int col = tn * 32 + c;
+    const bool interior = tm * 32 + 32 <= M && tn * 32 + 32 <= N;  // wave-uniform
+#pragma unroll
+    for (int j = 0; j < kShare; ++j) {
+        const int v = G > 1 ? g * kShare + j : j;
+        const int crow = tm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (interior || (crow < M && col < N)) C[size_t(crow) * N + col] = acc[j];
+    }
+}
+
+// LDS bytes of the LDS-staged direct kernel for G waves over `slices` K slices.
+uint32_t direct_lds_bytes(int g, int slices) {
+    return uint32_t(g) * uint32_t(dlds::ring((slices + g - 1) / g)) * dlds::kSlotB;
+}
+
+hipError_t launch_direct_lds(hipStream_t stream, int g, const float *a, const float *b, float *c, int m, int n,
+                             int k, int tiles_m, int tiles_n) {
+    const dim3 grid(unsigned(tiles_m * tiles_n)), block(unsigned(64 * g));
+    const int slices = (k + kBK - 1) / kBK, per_wave = (slices + g - 1) / g;
+    const bool whole = k % kBK == 0;
+    hipError_t status = hipErrorInvalidValue;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, block, 0, stream, a, b, c, m, n, k, tiles_m, tiles_n);
+        status = hipGetLastError();
+    };
+    auto with_s = [&](auto gc, auto wc) {
+        constexpr int G = decltype(gc)::value;
+        constexpr bool WH = decltype(wc)::value;
+        switch (per_wave) {
+            case 1: go(gemm_f32_direct_lds<G, 1, WH>); break;
+            case 2: go(gemm_f32_direct_lds<G, 2, WH>); break;
+            case 3: go(gemm_f32_direct_lds<G, 3, WH>); break;
+            case 4: go(gemm_f32_direct_lds<G, 4, WH>); break;
+            case 5: go(gemm_f32_direct_lds<G, 5, WH>); break;
+            case 6: go(gemm_f32_direct_lds<G, 6, WH>); break;
+            default: break;  // more slices per wave: not a direct plan
+        }
+    };
+    auto with_g = [&](auto wc) {
+        if (g == 4) with_s(std::integral_constant<int, 4>{}, wc);
+        else if (g == 2) with_s(std::integral_constant<int, 2>{}, wc);
+        else if (g == 1) with_s(std::integral_constant<int, 1>{}, wc);
+    };
+    if (whole)
+        with_g(std::true_type{});
+    else
+        with_g(std::false_type{});
+    return status;
+}
+
 hipError_t launch_direct(hipStream_t stream, dim3 grid, int g, bool bufa, const float *a, const float *b, float *c,
                          int m, int n, int k, int lda, int tiles_m, int tiles_n, size_t sa = 0, size_t sb = 0,
                          size_t sc = 0) {
@@ -1534,6 +1741,16 @@ bool big_fits(uint32_t m, uint32_t n, uint32_t k) {
     if (m % big::kBM != 0 || n % big::kBN != 0 || k % kBK != 0 || k == 0) return false;
     if (!dma_offsets_fit(big::kBM, big::kBN, k, n)) return false;
     return uint64_t(m / big::kBM) * (n / big::kBN) >= uint64_t(kCUs);
+}
+
+// The LDS-staged direct kernel serves unsplit direct plans with 16-byte rows
+// (K and N multiples of 4, A and B starting 16-byte aligned), at most one
+// workgroup per CU (up to 32 KiB of LDS per wave, 128 KiB per workgroup),
+// both operands below 2 GiB (32-bit buffer offsets) and at most six slices
+// per wave (direct_waves gives four waves from four slices up to 24).
+bool direct_lds_fits(uint32_t m, uint32_t n, uint32_t k, int tiles) {
+    return k % 4 == 0 && n % 4 == 0 && tiles <= kCUs && (k + kBK - 1) / kBK <= 4u * dlds::kMaxSlices &&
+           uint64_t(m) * k * 4u < (uint64_t(1) << 31) && uint64_t(k) * n * 4u < (uint64_t(1) << 31);
 }
 
 // Direct-load 32x32 tiles (one launch, K split over the four waves of a
@@ -1917,7 +2134,12 @@ LaunchShape gemm_f32_shape(uint32_t m, uint32_t n, uint32_t k) {
                                        "gemm_f32_direct_32x32x32_w4"};
         static const char *buf_names[3] = {"gemm_f32_direct_32x32x32_w1_buf", "gemm_f32_direct_32x32x32_w2_buf",
                                            "gemm_f32_direct_32x32x32_w4_buf"};
+        static const char *lds_names[3] = {"gemm_f32_direct_lds_32x32x32_w1", "gemm_f32_direct_lds_32x32x32_w2",
+                                           "gemm_f32_direct_lds_32x32x32_w4"};
         const int w = p.direct == 4 ? 2 : p.direct - 1;
+        if (p.slices == 1 && !p.bufa && direct_lds_fits(m, n, k, p.tiles_m * p.tiles_n))
+            return {lds_names[w], {uint32_t(p.tiles_m * p.tiles_n), 1, 1}, {uint32_t(64 * p.direct), 1, 1},
+                    direct_lds_bytes(p.direct, int((k + kBK - 1) / kBK))};
         return {p.slices > 1 ? "gemm_f32_direct_32x32x32_w4_splitk" : p.bufa ? buf_names[w] : names[w],
                 {uint32_t(p.tiles_m * p.tiles_n), uint32_t(p.slices), 1},
                 {uint32_t(64 * p.direct), 1, 1},
@@ -2070,6 +2292,8 @@ hipError_t gemm_f32(hipStream_t stream, const float *a, const float *b, float *c
                                p.slices);
             return hipGetLastError();
         }
+        if (!p.bufa && direct_lds_fits(m, n, k, p.tiles_m * p.tiles_n))
+            return launch_direct_lds(stream, p.direct, a, b, c, int(m), int(n), int(k), p.tiles_m, p.tiles_n);
         return launch_direct(stream, grid, p.direct, p.bufa, a, b, c, int(m), int(n), int(k), int(k), p.tiles_m,
                              p.tiles_n);
     }

@@ -130,3 +130,34 @@ def test_preheat_follows_the_command_line_value(bench, monkeypatch):
         work = bench.Workload(rt, [], 1)
         work.preheat()
         assert rt.calls == want_calls and work.preheat_ms >= target
+
+
+def test_short_workloads_sample_at_least_a_millisecond(bench, monkeypatch):
+    # Outside the headline a sample holds enough steps for MIN_SAMPLE_MS of
+    # device time (estimated from the pre-heat), so the idle queue's dispatch
+    # latency, paid once per sample, is spread over many launches; the
+    # headline (min_repeats 1) times exactly the requested steps.
+    class Execution:
+        def __init__(self, repeats):
+            self.gpu_ms = self.host_ms = 0.006 * repeats
+
+    class FakeRuntime:
+        def __init__(self):
+            self.calls = []
+
+        def execute(self, jobs, repeats):
+            self.calls.append(repeats)
+            return Execution(repeats)
+
+    monkeypatch.setattr(bench, "PREHEAT_MS", 5.0)
+    rt = FakeRuntime()
+    out = bench.measure({"w": bench.Workload(rt, [], 1)}, 50, 0)
+    assert out["w"]["sample_steps"] == [167] * bench.SAMPLES
+    assert out["w"]["ms_per_step"] == pytest.approx(0.006)
+    rt = FakeRuntime()
+    out = bench.measure({"w": bench.Workload(rt, [], 1)}, 50, 0, min_repeats=1)
+    assert sum(out["w"]["sample_steps"]) == 50
+    monkeypatch.setattr(bench, "PREHEAT_MS", 0.0)
+    rt = FakeRuntime()
+    out = bench.measure({"w": bench.Workload(rt, [], 1)}, 50, 0)
+    assert out["w"]["sample_steps"] == [10] * bench.SAMPLES

@@ -123,14 +123,19 @@ def test_edge_masking_shapes(runtime, m, n, k):
 
 @pytest.mark.parametrize("m,n,k,waves", [(300, 200, 100, 4), (384, 320, 768, 4), (130, 520, 388, 4),
                                           (257, 255, 36, 2), (64, 2048, 96, 2), (255, 257, 4, 1),
-                                          (700, 700, 700, 4), (2047, 33, 164, 4)])
+                                          (700, 700, 700, 4), (2047, 33, 164, 4), (512, 512, 512, 4),
+                                          (256, 256, 20, 1), (500, 300, 740, 4), (33, 4096, 36, 2)])
 def test_direct_tile_shapes(runtime, m, n, k, waves):
     # The direct-load 32x32 kernel: ragged M and N (clamped rows and columns that
     # are never stored), a partial last K slice (zeroed past K), one, two and
     # four waves per tile, and per-wave slice counts that leave 0, 1 or 2 slices
     # after the last whole round of three in flight.
+    # Grids of at most one tile per CU with 16-byte rows stage each wave's
+    # slices through LDS (a ring of four slots: K = 768 reuses two of them).
     kernel = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})
-    assert kernel.launch["kernel"] == f"gemm_f32_direct_32x32x32_w{waves}", kernel.launch
+    staged = ((m + 31) // 32) * ((n + 31) // 32) <= 256 and k % 4 == 0 and n % 4 == 0
+    want = f"gemm_f32_direct_lds_32x32x32_w{waves}" if staged else f"gemm_f32_direct_32x32x32_w{waves}"
+    assert kernel.launch["kernel"] == want, kernel.launch
     a = orc.values(m * k, 0x99, 1.0)
     b = orc.values(k * n, 0xAA, 1.0)
     got = run_gemm(runtime, m, n, k, a, b, repeats=2)

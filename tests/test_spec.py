@@ -167,7 +167,9 @@ def test_constant_bits_round_trip():
     (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k4", [208, 1, 1]),  # unaligned rows through buffer loads: four too
     (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),
     (1536, 1024, 1024, "gemm_f32_mfma_64x64x32", [384, 1, 1]),  # 256 < tiles < 384: one group
-    (512, 512, 512, "gemm_f32_direct_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K
+    (512, 512, 512, "gemm_f32_direct_lds_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K via LDS
+    (384, 384, 516, "gemm_f32_direct_lds_32x32x32_w4", [144, 1, 1]),  # ragged last slice
+    (512, 510, 512, "gemm_f32_direct_32x32x32_w4", [256, 1, 1]),  # N % 4 != 0: register-staged
     (700, 700, 700, "gemm_f32_direct_32x32x32_w4", [484, 1, 1]),  # 6 slices per wave
     (768, 768, 768, "gemm_f32_mfma_64x64x32_k4", [144, 1, 1]),  # > 128 64x64 tiles: not direct
     (255, 257, 4, "gemm_f32_direct_32x32x32_w1", [72, 1, 1]),  # one slice: one wave
@@ -321,7 +323,7 @@ def test_every_gemm_shape_routes_to_a_launch():
     families = {"gemm_f32_mfma_256x256x32_tail64x64", "gemm_f32_mfma_256x256x32_tail128x128",
                 "gemm_f32_direct_32x32x32_w4_buf", "gemm_f32_mfma_128x128x32", "gemm_f32_mfma_128x64x32",
                 "gemm_f32_mfma_64x64x32", "gemm_f32_mfma_64x64x32_k2", "gemm_f32_mfma_64x64x32_k4",
-                "gemm_f32_mfma_64x64x32_splitk_k2", "gemm_f32_direct_32x32x32_w4",
+                "gemm_f32_mfma_64x64x32_splitk_k2", "gemm_f32_direct_32x32x32_w4", "gemm_f32_direct_lds_32x32x32_w4",
                 "gemm_f32_direct_32x32x32_w4_splitk", "gemm_f32_ring_128x128x32"}
     assert families <= seen, families - seen
 
