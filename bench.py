@@ -429,6 +429,74 @@ def bench_floor(rt, steps, warmup):
     return out
 
 
+# The shapes set beside the vendor library: the headline, the large cubes, the
+# LLM-width product and the MLP's two GEMM shapes. Smaller products are left
+# out: torch.matmul's per-call host path (~19 us on the pool's hosts) then
+# bounds its back-to-back time, which would compare dispatch, not kernels.
+VENDOR_SHAPES = ((4096, 4096, 4096), (2048, 2048, 2048), (4096, 11008, 4096), (4096, 2816, 1024),
+                 (4096, 1024, 2816), (1024, 1024, 1024))
+VENDOR_ROUNDS = 3
+
+
+def bench_vendor(rt, steps, warmup, rounds=VENDOR_ROUNDS):
+    """This library's GEMM beside torch.matmul in FP32 (TF32 off; hipBLASLt
+    on ROCm) in one process, on the same validation::inputs, as the
+    reference's harness sets its kernel beside the platform library
+    (src/runtime/metal_lab.rs:150, native/jade_corex.cpp:91-95). Per shape,
+    `rounds` rounds alternate which side runs first; each round is SAMPLES
+    event-timed samples per side of at least MIN_SAMPLE_MS of device time
+    (this library: measure() on the runtime's stream; torch: back-to-back
+    calls on torch's stream). Reports the median over rounds of each round's
+    median, and the ratio library time / this library's time."""
+    import torch
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    out = {}
+    for m, n, k in VENDOR_SHAPES:
+        p = prepare_gemm(rt, m, n, k)
+        a = torch.from_numpy(jade_hip.fill_values(m * k, 0x12345678, 1.0).reshape(m, k)).to("cuda")
+        b = torch.from_numpy(jade_hip.fill_values(k * n, 0x9ABCDEF1, 1.0).reshape(k, n)).to("cuda")
+        c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+
+        def torch_ms(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(a, b, out=c)
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / reps
+
+        spent, reps = 0.0, 1
+        while spent < PREHEAT_MS:  # the library's own pre-heat
+            spent += torch_ms(reps) * reps
+            reps = min(2 * reps, 1 << 12)
+        per_call = torch_ms(SAMPLE_REPEATS)
+        reps = max(SAMPLE_REPEATS, int(math.ceil(MIN_SAMPLE_MS / max(per_call, 1e-6))))
+        ours, lib = [], []
+        for r in range(rounds):
+            for side in ((0, 1) if r % 2 == 0 else (1, 0)):
+                if side == 0:
+                    first = len(p.workload.samples)
+                    measure({"gemm": p.workload}, steps, warmup)
+                    ours.append(median(p.workload.samples[first:]))
+                else:
+                    lib.append(median([torch_ms(reps) for _ in range(SAMPLES)]))
+        kernel = p.info["kernel"]
+        p.close()
+        del a, b, c
+        flop = 2.0 * m * n * k
+        mo, ml = median(ours), median(lib)
+        out[f"{m}x{n}x{k}"] = {"ms": mo, "tflops": flop / (mo * 1e-3) / 1e12, "kernel": kernel,
+                               "vendor_ms": ml, "vendor_tflops": flop / (ml * 1e-3) / 1e12,
+                               "vendor_over_ours": ml / mo, "rounds_ms": ours, "vendor_rounds_ms": lib,
+                               "vendor_calls_per_sample": reps}
+        log(f"  {m}x{n}x{k}: {mo * 1e3:.2f} us ({kernel}) vs torch.matmul {ml * 1e3:.2f} us, "
+            f"ratio {ml / mo:.3f}")
+    out["vendor"] = f"torch {torch.__version__} torch.matmul FP32, TF32 off"
+    return out
+
+
 def _read_csv(path):
     import csv
 
@@ -463,7 +531,8 @@ def _workload_of(path):
 def bench_gemm_launches(bench_log):
     """(shape, launch kernel name, event-timed ms per launch) of every GEMM
     that a bench.py JSON line in `bench_log` reports: the headline, the MLP's
-    GEMMs launched alone and the sweep."""
+    GEMMs launched alone, the sweep and this library's side of the vendor
+    comparison."""
     line = None
     with open(bench_log, errors="replace") as f:
         for text in f:
@@ -481,7 +550,24 @@ def bench_gemm_launches(bench_log):
             out.append((op["shape"], op["kernel"], op["ms"]))
     for shape, r in extra.get("gemm_sweep", {}).items():
         out.append((shape, r["kernel"], r["ms"]))
+    for shape, r in extra.get("vendor_gemm", {}).items():
+        if isinstance(r, dict):
+            out.append((shape, r["kernel"], r["ms"]))
     return out
+
+
+def vendor_gemm_launches(bench_log):
+    """(shape, "vendor", event-timed ms per call) of the library side of a
+    `--workload vendor` line in `bench_log`."""
+    line = None
+    with open(bench_log, errors="replace") as f:
+        for text in f:
+            if text.startswith('{"metric"'):
+                line = json.loads(text)
+    if line is None:
+        return []
+    return [(shape, "vendor", r["vendor_ms"]) for shape, r in line.get("extra", {}).get("vendor_gemm", {}).items()
+            if isinstance(r, dict)]
 
 
 def split_by_shape(durations_ns, launches, tolerance=0.25):
@@ -517,13 +603,20 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None, bench_log=None)
         groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
     launches = bench_gemm_launches(bench_log) if bench_log else []
     ring_shapes = [x for x in launches if x[1].startswith("gemm_f32_ring")]
+    # The vendor library's GEMMs (hipBLASLt "Cijk_" kernels) also run one
+    # grid at several shapes; the same split applies against its medians.
+    vendor_shapes = vendor_gemm_launches(bench_log) if bench_log else []
     rows = []
     for key, durations in groups.items():
         if key[0].startswith("gemm_f32_ring") and ring_shapes:
-            for shape, part in split_by_shape(durations, ring_shapes).items():
-                rows.append((key[0] + (f" [{shape}]" if shape else " [unassigned]"), key[1:], part))
+            split = split_by_shape(durations, ring_shapes)
+        elif key[0].startswith("Cijk_") and vendor_shapes:
+            split = split_by_shape(durations, vendor_shapes)
         else:
             rows.append((key[0], key[1:], durations))
+            continue
+        for shape, part in split.items():
+            rows.append((key[0] + (f" [{shape}]" if shape else " [unassigned]"), key[1:], part))
     counters = {}
     for directory, counter in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
         if not directory:
@@ -730,7 +823,7 @@ def main():
                     help="untimed device time of each workload before its samples (0 for counter runs)")
     ap.add_argument("--workload", default="all",
                     choices=["all", "gemm", "attention", "softmax", "mlp", "rows", "sweep", "copy", "mfma", "floor",
-                             "shape"])
+                             "shape", "vendor"])
     ap.add_argument("--shape", default="4096x4096x2048", metavar="MxNxK",
                     help="the one GEMM of --workload shape (counter runs of one shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -772,6 +865,10 @@ def main():
         sys.exit("steps must be positive, warmup and preheat non-negative")
     PREHEAT_MS = args.preheat_ms
 
+    if args.workload == "vendor":
+        # torch's HIP runtime must be the process's first: loaded after this
+        # library's, its device init finds no GPU.
+        import torch  # noqa: F401
     rt = jade_hip.HipRuntime(0)
     log(f"device: {rt.device_info}")
     K, W, wl = args.steps, args.warmup, args.workload
@@ -822,6 +919,8 @@ def main():
                 f"{f['behind_full_queue_us']:.2f} us behind a full queue")
     if wl == "mfma":  # counter runs only; not part of the default line
         extra["mfma_shapes"] = bench_mfma_shapes(rt, K, W)
+    if wl == "vendor":  # this library beside torch.matmul; not part of the default line
+        extra["vendor_gemm"] = bench_vendor(rt, K, W)
     if wl == "shape":  # one GEMM shape (counter runs); not part of the default line
         m, n, k = (int(x) for x in args.shape.split("x"))
         r = bench_gemm(rt, m, n, k, K, W)

@@ -108,6 +108,21 @@ def test_persistent_gemm_rows_split_by_shape(bench, tmp_path):
                     "gemm_f32_ring<1, true> [2048x2048x2048]": "2", "gemm_f32_ring<1, true> [unassigned]": "2"}
 
 
+def test_vendor_workload_shapes_split_the_trace(bench, tmp_path):
+    # `--workload vendor` prints no headline: its line holds only `extra`, and
+    # this library's side of each shape names the shapes the trace rows of
+    # the persistent kernel are split by. The string entry is not a shape.
+    line = {"metric": "m", "workload": "vendor",
+            "extra": {"vendor_gemm": {"4096x4096x4096": {"ms": 0.915, "kernel": "gemm_f32_ring_128x128x32"},
+                                      "1024x1024x1024": {"ms": 0.0205, "kernel": "gemm_f32_mfma_64x64x32_k4"},
+                                      "vendor": "torch.matmul FP32"}}}
+    log = tmp_path / "vendor.log"
+    log.write_text(__import__("json").dumps(line) + "\n")
+    assert bench.bench_gemm_launches(str(log)) == [("4096x4096x4096", "gemm_f32_ring_128x128x32", 0.915),
+                                                   ("1024x1024x1024", "gemm_f32_mfma_64x64x32_k4", 0.0205)]
+    assert set(bench.VENDOR_SHAPES) >= {(4096, 4096, 4096), (4096, 1024, 2816), (4096, 2816, 1024)}
+
+
 def test_preheat_follows_the_command_line_value(bench, monkeypatch):
     # --preheat-ms replaces the module-level PREHEAT_MS after the classes are
     # defined; the pre-heat must read it when it runs.
