@@ -11,12 +11,16 @@ sweep and the copy calibration.
 Timing follows the reference's harness (src/runtime/metal_lab.rs:75-107,
 179-187): each workload gets W untimed warm-up steps and a time-based
 pre-heat (--preheat-ms of device time, reported as `preheat_ms`), then nine
-samples, interleaved with the other headline workload in rotating order, each
-timed by hipEvents around its launches on the runtime's stream (the
-jr_execute scope, native/jade_runtime_corex.cpp:148-189). The headline's
-samples split exactly K timed steps; every other workload's samples hold at
-least the reference's ten repeats each. The reported per-step time is the
-median sample; the mean and the extremes are listed beside it. Bandwidth-bound ops are rotated over copies of
+consecutive samples, each timed by hipEvents around its launches on the
+runtime's stream (the jr_execute scope,
+native/jade_runtime_corex.cpp:148-189). The headline's samples split exactly
+K timed steps; every other workload's samples hold at least the reference's
+ten repeats each. The reported per-step time is the median sample; the mean
+and the extremes are listed beside it. The two headline workloads are not
+interleaved: after a few milliseconds of the attention kernel, the first
+three to four 4096^3 GEMMs run 1-1.5% slower while the clock recovers
+(kernel trace of the default line), so a GEMM sample of two or three steps
+placed after each attention sample measured that transient. Bandwidth-bound ops are rotated over copies of
 their buffers that exceed the 256 MB MALL three times, so their GB/s are HBM
 figures.
 
@@ -630,11 +634,14 @@ def summarize_rocprof(trace_dir, fetch_dir=None, write_dir=None, bench_log=None)
                 key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]),
                        _workload_of(path))
                 counters.setdefault(key, {}).setdefault(counter, []).append(float(row["Counter_Value"]))
-    lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us |",
-             "|---|---|---|---|---|---|---|"]
+    # The median beside the mean: a workload's dispatches include its
+    # pre-heat, whose first launches run at a lower clock.
+    lines = ["| kernel | grid (work-items) | block | calls | avg us | min us | max us | median us |",
+             "|---|---|---|---|---|---|---|---|"]
     for name, (gx, gy, gz, wg), durations in sorted(rows, key=lambda r: -sum(r[2])):
         lines.append(f"| {name} | {gx}x{gy}x{gz} | {wg} | {len(durations)} | {np.mean(durations) / 1e3:.2f} | "
-                     f"{np.min(durations) / 1e3:.2f} | {np.max(durations) / 1e3:.2f} |")
+                     f"{np.min(durations) / 1e3:.2f} | {np.max(durations) / 1e3:.2f} | "
+                     f"{np.median(durations) / 1e3:.2f} |")
     if ring_shapes:
         lines += ["", "Event-timed medians of the same run (bench.py's own figures, ms per launch): " +
                   ", ".join(f"{shape} {ms * 1e3:.2f} us ({kernel})" for shape, kernel, ms in launches)]
@@ -876,14 +883,16 @@ def main():
     gemm = attention = None
     keep = not args.no_cpu_baseline
     if wl in ("all", "gemm", "attention"):
-        # The two headline kernels, sampled interleaved (round r rotates the order).
+        # The two headline kernels, each sampled on its own after its pre-heat.
         heads = {}
         if wl in ("all", "gemm"):
             heads["gemm"] = prepare_gemm(rt, 4096, 4096, 4096, keep)
         if wl in ("all", "attention"):
             heads["attention"] = prepare_attention(rt, 128, 4096, 128, True, keep)
         log(f"headline {', '.join(heads)} ...")
-        timing = measure({name: p.workload for name, p in heads.items()}, K, W, min_repeats=1)
+        timing = {}
+        for name, p in heads.items():
+            timing.update(measure({name: p.workload}, K, W, min_repeats=1))
         if "gemm" in heads:
             gemm = finish_gemm(rt, heads["gemm"], timing["gemm"])
             log(f"  gemm 4096^3 {gemm['tflops']:.2f} TFLOP/s")
@@ -966,7 +975,7 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": config,
-        "timing": {"method": f"median of {head['samples']} interleaved samples over exactly the {K} timed steps, after "
+        "timing": {"method": f"median of {head['samples']} consecutive samples over exactly the {K} timed steps, after "
                              f"{W} warm-up steps and a {PREHEAT_MS:.0f} ms time-based pre-heat per workload",
                    "median_ms_per_step": head["ms_per_step"], "mean_ms_per_step": head["mean_ms_per_step"],
                    "min_ms_per_step": head["min_ms_per_step"], "max_ms_per_step": head["max_ms_per_step"],
