@@ -6,7 +6,9 @@
 // cols <= 4096) it is read from HBM exactly once and written once; the
 // reductions are wavefront butterflies with no LDS and no barrier. Output rows
 // go out as non-temporal vector stores (no L2 allocation for a stream that is
-// not re-read here).
+// not re-read here), and the cached kernels read their rows through
+// non-temporal loads as well (RMSNorm 4096x1024 streamed from HBM: 6.42 ->
+// 5.96 us); the weight row, shared by every row, keeps ordinary loads.
 #include "kernels.hpp"
 
 #include <cmath>
@@ -48,7 +50,7 @@ __global__ __launch_bounds__(kThreads) void rms_norm_cached(const float *__restr
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
         const int idx = lane + 64 * i;
-        v[i] = idx < n4 ? xr[idx] : f32x4{0.f, 0.f, 0.f, 0.f};
+        v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{0.f, 0.f, 0.f, 0.f};
         sum = fmaf(v[i].x, v[i].x, sum);
         sum = fmaf(v[i].y, v[i].y, sum);
         sum = fmaf(v[i].z, v[i].z, sum);
@@ -92,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void softmax_cached(const float *__restri
 #pragma unroll
     for (int i = 0; i < C4; ++i) {
         const int idx = lane + 64 * i;
-        v[i] = idx < n4 ? xr[idx] : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        v[i] = idx < n4 ? __builtin_nontemporal_load(xr + idx) : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
     }
     m = wave_max(m);

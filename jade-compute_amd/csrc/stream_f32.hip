@@ -6,7 +6,10 @@
 // length that is not a multiple of 4 falls back to scalar accesses. Vector
 // results go out as non-temporal stores: the written stream is not re-read by
 // the same kernel, and skipping L2 allocation took a 256 MiB copy from 6.05 to
-// 7.38 TB/s on MI355X.
+// 7.38 TB/s on MI355X. The inputs are read once too and come in through
+// non-temporal loads: Add over 4096x1024 (50 MB per launch, streamed from
+// HBM) 10.15 -> 9.49 us, 4096x2816 (138 MB) 23.8 -> 22.1 us. More slots per
+// thread (2, 4, 8, block-strided) were slower at both sizes.
 #include "kernels.hpp"
 #include "ops.hpp"
 
@@ -38,8 +41,8 @@ __global__ __launch_bounds__(kThreads) void binary_stream(const float *__restric
     const uint32_t first = slot * 4u;
     if (first >= len) return;
     if (first + 4u <= len) {
-        const f32x4 x = reinterpret_cast<const f32x4 *>(a)[slot];
-        const f32x4 y = reinterpret_cast<const f32x4 *>(b)[slot];
+        const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a) + slot);
+        const f32x4 y = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(b) + slot);
         __builtin_nontemporal_store(f32x4{f(x.x, y.x), f(x.y, y.y), f(x.z, y.z), f(x.w, y.w)},
                                     reinterpret_cast<f32x4 *>(out) + slot);
     } else {
@@ -53,7 +56,8 @@ __global__ __launch_bounds__(kThreads) void copy_stream(const float *__restrict_
     const uint32_t first = slot * 4u;
     if (first >= len) return;
     if (first + 4u <= len) {
-        __builtin_nontemporal_store(reinterpret_cast<const f32x4 *>(in)[slot], reinterpret_cast<f32x4 *>(out) + slot);
+        __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(in) + slot),
+                                    reinterpret_cast<f32x4 *>(out) + slot);
     } else {
         for (uint32_t i = first; i < len; ++i) out[i] = in[i];
     }
