@@ -53,8 +53,8 @@ def log(msg):
 
 
 # The reference's harness method (src/runtime/metal_lab.rs:75-107,179-187;
-# reports/METAL_ADVANCES.md:109-120): warm up, then interleaved samples,
-# report the median per-step time. Here every workload also gets a time-based
+# reports/METAL_ADVANCES.md:109-120): warm up, then samples (interleaved when
+# several workloads are measured together), report the median per-step time. Here every workload also gets a time-based
 # pre-heat before its samples: the MI355X clock ramps over the first ~30 ms of
 # sustained matrix work, which a fixed warm-up count does not cover for short
 # launches.
@@ -703,16 +703,24 @@ def summarize_mfma(directory):
     """MFMA busy share per (kernel, grid, workload) from rocprofv3 --pmc runs
     with SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE, one output directory per
     bench.py workload: busy / (GUI cycles per XCD x SIMDs). GRBM_GUI_ACTIVE is
-    summed over the 8 XCDs."""
+    summed over the 8 XCDs. The GUI clock column is GUI cycles per XCD over the
+    dispatch's own duration (its start and end timestamps), median over
+    dispatches: the clock during launches long enough that launch and drain
+    are a small part of them."""
     vals = {}
     for path in _find_all(directory, "counter_collection.csv"):
         for row in _read_csv(path):
             key = (_short(row["Kernel_Name"]), int(row["Grid_Size"]), int(row["Workgroup_Size"]),
                    _workload_of(path))
-            vals.setdefault(key, {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+            per = vals.setdefault(key, {})
+            per.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+            if row["Counter_Name"] == "GRBM_GUI_ACTIVE" and "End_Timestamp" in row:
+                ns = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+                if ns > 0:
+                    per.setdefault("_ghz", []).append(float(row["Counter_Value"]) / XCDS / ns)
     lines = ["| kernel | workload | grid (work-items) | block | dispatches | GRBM_GUI_ACTIVE / XCD "
-             "| SQ_VALU_MFMA_BUSY_CYCLES | MFMA busy |",
-             "|---|---|---|---|---|---|---|---|"]
+             "| SQ_VALU_MFMA_BUSY_CYCLES | MFMA busy | GUI clock GHz |",
+             "|---|---|---|---|---|---|---|---|---|"]
     for key, v in sorted(vals.items()):
         if "SQ_VALU_MFMA_BUSY_CYCLES" not in v or "GRBM_GUI_ACTIVE" not in v:
             continue
@@ -721,8 +729,9 @@ def summarize_mfma(directory):
         if busy <= 0:
             continue
         flag = " (saturated)" if busy >= 2.0 ** 31 else ""
+        ghz = f"{np.median(v['_ghz']):.3f}" if v.get("_ghz") else "-"
         lines.append(f"| {key[0]} | {key[3]} | {key[1]} | {key[2]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | "
-                     f"{busy:.4g}{flag} | {100.0 * busy / (gui * SIMDS):.1f}% |")
+                     f"{busy:.4g}{flag} | {100.0 * busy / (gui * SIMDS):.1f}% | {ghz} |")
     return "\n".join(lines)
 
 
