@@ -123,6 +123,24 @@ def test_vendor_workload_shapes_split_the_trace(bench, tmp_path):
     assert set(bench.VENDOR_SHAPES) >= {(4096, 4096, 4096), (4096, 1024, 2816), (4096, 2816, 1024)}
 
 
+def test_mfma_summary_reports_busy_share_and_clock(bench, tmp_path):
+    # Eight XCDs of 2.4e6 GUI cycles each over a 1 ms dispatch: 2.4 GHz. Busy
+    # cycles of 0.9 x 2.4e6 per SIMD on 1024 SIMDs: 90% busy.
+    name = SYMBOL.format("gemm_f32_ring<1, true>")
+    rows = []
+    for dispatch in range(3):
+        start = 10_000_000 * dispatch
+        for counter, value in (("GRBM_GUI_ACTIVE", 8 * 2.4e6), ("SQ_VALU_MFMA_BUSY_CYCLES", 0.9 * 2.4e6 * 1024)):
+            rows.append({"Dispatch_Id": dispatch, "Kernel_Name": name, "Grid_Size": 131072, "Workgroup_Size": 512,
+                         "Counter_Name": counter, "Counter_Value": value, "Start_Timestamp": start,
+                         "End_Timestamp": start + 1_000_000})
+    write_csv(str(tmp_path / "pmc" / "4096x4096x2048" / "run_counter_collection.csv"), rows)
+    line = [ln for ln in bench.summarize_mfma(str(tmp_path / "pmc")).splitlines() if ln.startswith("| gemm")][0]
+    cells = [x.strip() for x in line.split("|")[1:-1]]
+    assert cells[1] == "4096x4096x2048" and cells[4] == "3"
+    assert cells[7] == "90.0%" and cells[8] == "2.400"
+
+
 def test_preheat_follows_the_command_line_value(bench, monkeypatch):
     # --preheat-ms replaces the module-level PREHEAT_MS after the classes are
     # defined; the pre-heat must read it when it runs.
