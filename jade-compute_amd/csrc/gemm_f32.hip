@@ -16,10 +16,11 @@
 //    gemm_f32_mfma_256 (one 512-thread workgroup per CU, eight waves of
 //    128x64) plus a partial round of 128x128 or 64x64 tiles.
 //  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
-//    LDS-direct loads (interior tiles) or a register prefetch (edge tiles and
-//    unaligned shapes; unaligned 64x64 and 128x64 tiles keep two stages in
-//    registers, loaded through buffer instructions), with one barrier per
-//    stage.
+//    LDS-direct loads: global loads for interior tiles, range-checked buffer
+//    loads for edge tiles and for unaligned rows over whole stages. K ranges
+//    with a partial stage, and operands too long for 32-bit offsets, take a
+//    register prefetch (unaligned 64x64 and 128x64 tiles keep two stages in
+//    registers, loaded through buffer instructions). One barrier per stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
@@ -133,11 +134,12 @@ __device__ inline void issue_stage_dma_part(const float *__restrict__ A, const f
     }
 }
 
-// Edge tiles of aligned shapes: the same stage through 16-byte buffer loads
-// into LDS (buffer_load_dwordx4 ... lds), whose range check returns zero past
-// the end of A (rows past M) and of B, so no bounds branch is needed. B runs
-// past N read the next row's first columns, which feed only unstored outputs.
-// Whole stages only (k stays below K). `ra` and `rb` cover A and B.
+// Edge tiles of aligned shapes, and tiles of unaligned shapes: the same stage
+// through 16-byte buffer loads into LDS (buffer_load_dwordx4 ... lds) at
+// 4-byte-aligned offsets, whose range check returns zero past the end of A
+// (rows past M) and of B, so no bounds branch is needed. B runs past N read
+// the next row's first columns, which feed only unstored outputs. Whole
+// stages only (k stays below K). `ra` and `rb` cover A and B.
 template <int TM, int TN>
 __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int N, int K, int m0,
                                        int n0, int k0, float *stage, int t) {
@@ -709,8 +711,9 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 // only the LDS-direct loop is compiled in (fewer registers, tighter code).
 // kRegOnly: register-staged loads (64-bit addresses) for every tile, for
 // operands too long for the LDS-direct loads' 32-bit offsets.
-// kUnalignedBuf: unaligned rows (no 16-byte loads) through buffer loads,
-// for 64x64 and 128x64 tiles over operands below 2 GiB each.
+// kUnalignedBuf: unaligned rows (no 16-byte-aligned loads) through buffer
+// loads, for 64x64 and 128x64 tiles over operands below 2 GiB each: into LDS
+// directly over whole stages, else staged in registers.
 enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2, kUnalignedBuf = 3 };
 
 // LDS-direct loads address each lane's 16 bytes as a 32-bit byte offset from
@@ -840,15 +843,25 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     }
 
     // Interior tiles with 16-byte rows stream through LDS-direct loads; edge
-    // tiles, unaligned shapes and K ranges that are not KG x nk whole stages
-    // take the guarded, register-staged path.
-    const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && klast - kfirst == KG * nk * kBK;
+    // tiles and unaligned shapes over whole stages take the same loop through
+    // buffer loads; K ranges that are not KG x nk whole stages take the
+    // guarded, register-staged path.
+    const bool whole = kmain - kfirst == KG * nk * kBK;
+    const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && whole;
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
-    // Edge tiles of aligned shapes with whole stages: the same loop through
-    // range-checked buffer loads (operands whose 32-bit offsets, with a tile
-    // of rows past M, stay below 2 GiB).
-    else if (PATH == kMixed && VEC && klast - kfirst == KG * nk * kBK &&
+    // Edge tiles of aligned shapes, and every tile of an unaligned shape, with
+    // whole stages: the same loop through range-checked buffer loads
+    // (operands whose 32-bit offsets, with a tile of rows past M, stay below
+    // 2 GiB). The 16-byte runs of unaligned rows start at 4-byte-aligned
+    // offsets, which buffer loads into LDS take as they are; whole stages
+    // keep every A run inside its row, and a B run past N reads the next
+    // row's first columns (zero past the end of B), which feed only
+    // outputs that are never stored. Against the register-staged loop
+    // (us): 1000x777x513 13.78 -> 13.59, 1000x777x512 13.28 -> 12.86,
+    // 1000x777x1025 23.22 -> 22.20, 2048x2047x2048 144.1 -> 135.5,
+    // 3000x3001x3008 533.8 -> 506.4.
+    else if (((PATH == kMixed && VEC) || PATH == kUnalignedBuf) && whole &&
              (uint64_t(M) + T::kBM) * uint64_t(K) * 4u < (uint64_t(1) << 31) &&
              (uint64_t(K) + 1) * uint64_t(N) * 4u + T::kBN * 4u < (uint64_t(1) << 31))
         k_loop_dma<TM, TN, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);

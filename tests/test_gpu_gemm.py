@@ -221,8 +221,27 @@ def test_unaligned_tail_k_in_the_epilogue(runtime, m, n, k, kernel):
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
+    (1000, 777, 512, "gemm_f32_mfma_64x64x32_k2"),  # the last B row's last run crosses the end of B
+    (1000, 1001, 1024, "gemm_f32_mfma_64x64x32_k4"),
+    (2000, 1555, 1024, "gemm_f32_mfma_128x64x32"),
+    (777, 1000, 770, "gemm_f32_mfma_64x64x32_k4"),  # K unaligned: 24 whole stages, two k in the epilogue
+])
+def test_unaligned_whole_stages_through_buffer_loads_into_lds(runtime, m, n, k, kernel):
+    # Unaligned rows over whole stages load 16-byte runs at 4-byte-aligned
+    # offsets straight into LDS (buffer_load_dwordx4 ... lds): A runs stay in
+    # their row, a B run past N reads the next row's first columns (past the
+    # end of B, zero from the range check), rows past M read zero.
+    launch = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch
+    assert launch["kernel"] == kernel, launch
+    a = orc.values(m * k, 0xB7, 1.0)
+    b = orc.values(k * n, 0xC7, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    gate(got, m, n, k, a, b)
+
+
+@pytest.mark.parametrize("m,n,k,kernel", [
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
-    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # register-staged (unaligned), last group partial
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows into LDS over 16 whole stages, k = 512 in the epilogue
     (1000, 777, 700, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows, K below the four-group threshold
     (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial
     (65, 67, 63, "gemm_f32_mfma_64x64x32_k2"),  # one stage per group
@@ -245,11 +264,11 @@ def test_two_group_tile_shapes(runtime, m, n, k, kernel):
 @pytest.mark.parametrize("m,n,k", [
     (1024, 1024, 1024),  # LDS-direct stages, 8 per group
     (768, 768, 768),  # 6 stages per group
-    (1000, 1000, 1024),  # edge tiles register-staged (16-byte rows), interior LDS-direct
+    (1000, 1000, 1024),  # edge tiles through buffer loads into LDS (16-byte rows), interior LDS-direct
     (1000, 600, 1000),  # 32 stages, the last partial: every tile register-staged
     (768, 768, 2048),  # 16 stages per group
-    (1000, 777, 1024),  # unaligned rows through buffer loads
-    (1023, 1000, 2049),  # unaligned rows, the last group's last stage partial
+    (1000, 777, 1024),  # unaligned rows through buffer loads into LDS
+    (1023, 1000, 2049),  # unaligned rows, the last group's last stage partial: register-staged
 ])
 def test_four_group_tile_shapes(runtime, m, n, k):
     # 64x64 tiles whose four K groups of four waves each sum a quarter of the

@@ -8,7 +8,9 @@ U hand-off touch, lies inside its buffer, for both of its tiles (128x64, and
 map covers every output exactly once. The kernel's index formulas are
 restated with numpy over all lanes, waves, instructions and stages, so a
 launch that the fusion rule accepts cannot address memory outside the
-bindings or the 64 KiB of LDS it declares."""
+bindings or the 64 KiB of LDS it declares. The tile kernel's buffer loads
+into LDS over unaligned rows are checked the same way: every run that feeds
+a stored output holds its own row's elements of the K range."""
 import numpy as np
 import pytest
 
@@ -222,3 +224,73 @@ def test_tile_columns_cover_the_tile_once(tn):
             for w in range(2):
                 chunks = {((int(x) >> 2) ^ swz_b(krow)) for x in cols[w, 0, :]}
                 assert len(chunks) == 16 and len({ch // 16 for ch in chunks}) == 1
+
+
+# The four-wave tile kernel (gemm_f32_mfma) over unaligned rows: whole
+# stages go through issue_stage_buf, 16-byte buffer loads into LDS at
+# 4-byte-aligned byte offsets (m0 + row) * K + k0 + 4j for A and
+# (k0 + row) * N + n0 + 4j for B, with a range check at M*K*4 and K*N*4.
+TILE_WAVES = 4
+
+
+def tile_buf_loads(tm, tn):
+    """(row, first column) of every 16-byte run one 256-thread group loads
+    into a stage of the (64 tm) x (64 tn) tile, for A and for B, and the LDS
+    byte each run lands at (issue_stage_buf<TM, TN>)."""
+    bm, bn = 64 * tm, 64 * tn
+    a_inst, b_inst = bm * BK * 4 // 1024 // TILE_WAVES, BK * bn * 4 // 1024 // TILE_WAVES
+    wave = np.arange(TILE_WAVES)[:, None, None]
+    lane = np.arange(LANES)[None, :, None]
+    inst = wave * a_inst + np.arange(a_inst)[None, None, :]
+    row = inst * 8 + (lane >> 3)
+    a = (row, 4 * ((lane & 7) ^ swz_a(row)), inst * 1024 + lane * 16)
+    chunks = bn // 4
+    inst = wave * b_inst + np.arange(b_inst)[None, None, :]
+    row = inst * (64 // chunks) + lane // chunks
+    b = (row, 4 * ((lane % chunks) ^ swz_b(row)), bm * BK * 4 + inst * 1024 + lane * 16)
+    return a, b
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 777, 513), (1000, 777, 512), (1000, 777, 1025), (777, 1000, 770),
+                                   (1000, 1001, 1024), (2000, 1555, 1024), (2048, 2047, 2048),
+                                   (3000, 3001, 3008)])
+def test_unaligned_whole_stages_load_inside_their_rows(m, n, k):
+    """Every run an unaligned whole-stage tile loads for an output that is
+    stored holds exactly the A row's or B row's own elements of the group's
+    K range; runs for rows past M lie past the end of A (the range check
+    returns zero), and B runs past N feed only columns past N. The plan
+    (tile, K groups, epilogue k) is the library's own launch description."""
+    import jade_hip
+    launch = jade_hip.spec_describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
+    name = launch["kernel"]
+    assert name.startswith("gemm_f32_mfma_") and launch["grid"][1] == 1, name
+    dims = name.split("_")[3]
+    bm, bn = int(dims.split("x")[0]), int(dims.split("x")[1])
+    last = name.split("_")[-1]
+    kg = int(last[1:]) if last.startswith("k") else 1
+    assert launch["block"][0] == 256 * kg
+    kmain = k - launch.get("epilogue_k", 0)
+    nk = -(-(-(-kmain // BK)) // kg)
+    # The kernel's condition for this loop: whole stages, 32-bit offsets.
+    assert kmain == kg * nk * BK
+    assert (m + bm) * k * 4 < 2 ** 31 and (k + 1) * n * 4 + bn * 4 < 2 ** 31
+    (a_row, a_col, a_lds), (b_row, b_col, b_lds) = tile_buf_loads(bm // 64, bn // 64)
+    # Each stage's LDS bytes are written once, A then B.
+    lds = np.concatenate([a_lds.ravel(), b_lds.ravel()])
+    assert np.array_equal(np.sort(lds), np.arange(0, (bm + bn) * BK * 4, 16))
+    m0 = (np.arange(-(-m // bm)) * bm)[:, None, None, None]
+    n0 = (np.arange(-(-n // bn)) * bn)[:, None, None, None]
+    k0 = (np.arange(kg * nk) * BK)[None, :, None, None]    # every group's stages
+    for e in range(4):
+        # A: element (m0 + row, k0 + col + e) at float offset (m0 + row) K + k0 + col + e.
+        rows, cols = np.broadcast_arrays(m0 + a_row.reshape(1, 1, -1, 1), k0 + a_col.reshape(1, 1, -1, 1) + e)
+        off = rows * k + cols
+        assert off.max() * 4 < 2 ** 32                      # no 32-bit wrap
+        assert (cols[rows < m] < kmain).all()
+        assert (off[rows >= m] >= m * k).all()
+        # B: element (k0 + row, n0 + col + e) where that column is below N.
+        rows, cols = np.broadcast_arrays(k0 + b_row.reshape(1, 1, -1, 1), n0 + b_col.reshape(1, 1, -1, 1) + e)
+        off = rows * n + cols
+        assert off.max() * 4 < 2 ** 32
+        assert rows.max() < kmain
+        assert (off[cols < n] < k * n).all()
