@@ -325,9 +325,15 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // The matrix cores sum kFoldStages stages into `part` before each fold into
 // acc (four against two: 4096^3 139.0 -> 141.1 TFLOP/s, 2048^3 131.8 ->
 // 133.9; the worst 4096^3 output then used 20% of the 1e-4 tolerance against
-// 17.5%; eight timed the same as four here). `nk` whole stages from kbegin; `t` is the thread's index in its 256-thread
-// group (every group of a workgroup runs the same number of stages, so the
-// barriers match).
+// 17.5%; eight timed the same as four here). The fold sits only at a run's
+// last stage, and a last, shorter run folds after the loop: a fold guarded by
+// "or this is the last stage" was if-converted into an add and a select after
+// every stage, whose reads of `part` waited for each stage's last MFMA (the
+// MFMA pipeline drained every stage, not every fourth): 1024x832x512 11.91 ->
+// 11.42 us, 2000x3000x1024 116.8 -> 108.4, 3000x3001x3008 505.7 -> 462.1,
+// the same bits. `nk` whole stages from kbegin; `t` is the thread's index in
+// its 256-thread group (every group of a workgroup runs the same number of
+// stages, so the barriers match).
 template <int TM, int TN, bool BUF = false>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
                                   int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
@@ -384,7 +390,7 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                     else
                         mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
                 }
-                if (uu == kFoldStages - 1 || k + 1 == nk) {
+                if (uu == kFoldStages - 1) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -395,6 +401,12 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 __syncthreads();
             }
         }
+    }
+    if (nk % kFoldStages != 0) {  // the last, shorter run
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
     }
 }
 
@@ -687,7 +699,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                     mma_stage<TM, TN, true>(cur, wm, wn, lane, part);
                 else
                     mma_stage<TM, TN, false>(cur, wm, wn, lane, part);
-                if (!PAIRS || u == 1 || k + 1 == nk) {
+                if (!PAIRS || u == 1) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -698,6 +710,12 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
                 lds_barrier();
             }
         }
+    }
+    if (PAIRS && nk % 2 != 0) {  // the last pair held one stage
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
     }
     keep_live(r[0]);
     keep_live(r[1]);
@@ -1056,7 +1074,7 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
                     mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
                 else
                     mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
-                if (uu == FOLD - 1 || k + 1 == nk) {
+                if (uu == FOLD - 1) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
                 }
@@ -1065,6 +1083,10 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
                 __syncthreads();
             }
         }
+    }
+    if (nk % FOLD != 0) {  // the last, shorter run
+#pragma unroll
+        for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
     }
     // The loop ended on a barrier: the stage buffers are free for U.
     const int h = lane >> 5, c = lane & 31;
