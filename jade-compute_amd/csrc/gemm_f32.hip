@@ -440,7 +440,7 @@ __device__ inline void k_loop(const float *__restrict__ A, const float *__restri
                     mma_stage<TM, TN, true>(cur, wm, wn, lane, part);
                 else
                     mma_stage<TM, TN, false>(cur, wm, wn, lane, part);
-                if (u == 1 || !more || !kPairs) {
+                if (u == 1 || !kPairs) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -450,6 +450,12 @@ __device__ inline void k_loop(const float *__restrict__ A, const float *__restri
                 __syncthreads();
             }
         }
+    }
+    if (kPairs && nk % 2 != 0) {  // the last pair held one stage
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] += part[i][j];
     }
 }
 
