@@ -2002,7 +2002,15 @@ Plan plan_tiles(uint32_t m, uint32_t n, uint32_t k) {
     }
     if (p.kchunk >= 2 * kBK) p.kgroups = 2;
     const bool rows16 = k % 4 == 0 && n % 4 == 0;
-    if (p.slices == 1 && p.kchunk >= kFourGroupMinK && (rows16 || unaligned_buffers_fit(m, n, k))) p.kgroups = 4;
+    // Unaligned rows whose K is whole stages that four groups split evenly
+    // (plus at most kMaxTail last k, added in the epilogue) load straight
+    // into LDS; there four groups beat two from K = 512 (1000x777x513 13.20
+    // -> 12.88 us, 1000x1000x513 13.43 -> 13.09, 1000x777x512 12.40 ->
+    // 12.31), while aligned rows keep two below kFourGroupMinK (1024x832x512
+    // 11.43 against 11.70 with four).
+    const bool whole4 = !rows16 && k >= 512 && (k / kBK) % 4 == 0 && k % kBK <= uint32_t(kMaxTail);
+    if (p.slices == 1 && (p.kchunk >= kFourGroupMinK || whole4) && (rows16 || unaligned_buffers_fit(m, n, k)))
+        p.kgroups = 4;
     return p;
 }
 

@@ -186,8 +186,8 @@ def test_unaligned_rows_keep_non_finite_values_in_place(runtime, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
-    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # 16 whole stages, 8 per group; k = 512 in the epilogue
-    (1000, 777, 514, "gemm_f32_mfma_64x64x32_k2"),  # two tail k
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k4"),  # 16 whole stages, 4 per group; k = 512 in the epilogue
+    (1000, 777, 514, "gemm_f32_mfma_64x64x32_k4"),  # two tail k
     (1000, 777, 545, "gemm_f32_mfma_64x64x32_k2"),  # 17 whole stages: the partial stage stays in the loop
     (1000, 777, 769, "gemm_f32_mfma_64x64x32_k4"),  # 24 whole stages over four groups, one tail k
     (1000, 777, 1027, "gemm_f32_mfma_64x64x32_k4"),  # three last k: more than the epilogue takes
@@ -221,7 +221,8 @@ def test_unaligned_tail_k_in_the_epilogue(runtime, m, n, k, kernel):
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
-    (1000, 777, 512, "gemm_f32_mfma_64x64x32_k2"),  # the last B row's last run crosses the end of B
+    (1000, 777, 512, "gemm_f32_mfma_64x64x32_k4"),  # the last B row's last run crosses the end of B
+    (1000, 777, 257, "gemm_f32_mfma_64x64x32_k2"),  # 8 whole stages over two groups, k = 256 in the epilogue
     (1000, 1001, 1024, "gemm_f32_mfma_64x64x32_k4"),
     (2000, 1555, 1024, "gemm_f32_mfma_128x64x32"),
     (777, 1000, 770, "gemm_f32_mfma_64x64x32_k4"),  # K unaligned: 24 whole stages, two k in the epilogue
@@ -241,7 +242,6 @@ def test_unaligned_whole_stages_through_buffer_loads_into_lds(runtime, m, n, k, 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
-    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows into LDS over 16 whole stages, k = 512 in the epilogue
     (1000, 777, 700, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows, K below the four-group threshold
     (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial
     (65, 67, 63, "gemm_f32_mfma_64x64x32_k2"),  # one stage per group
@@ -268,6 +268,7 @@ def test_two_group_tile_shapes(runtime, m, n, k, kernel):
     (1000, 600, 1000),  # 32 stages, the last partial: every tile register-staged
     (768, 768, 2048),  # 16 stages per group
     (1000, 777, 1024),  # unaligned rows through buffer loads into LDS
+    (1000, 777, 513),  # unaligned rows into LDS, 4 whole stages per group, k = 512 in the epilogue
     (1023, 1000, 2049),  # unaligned rows, the last group's last stage partial: register-staged
 ])
 def test_four_group_tile_shapes(runtime, m, n, k):

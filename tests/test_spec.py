@@ -165,7 +165,8 @@ def test_constant_bits_round_trip():
     (1024, 1024, 1024, "gemm_f32_mfma_64x64x32_k4", [256, 1, 1]),  # <= 256 tiles, K >= 768: four K groups
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2", [256, 1, 1]),  # shorter K: two K groups
     (1000, 777, 1024, "gemm_f32_mfma_64x64x32_k4", [208, 1, 1]),  # unaligned rows through buffer loads: four too
-    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),
+    (1000, 777, 513, "gemm_f32_mfma_64x64x32_k4", [208, 1, 1]),  # unaligned, whole stages four groups split
+    (1000, 777, 545, "gemm_f32_mfma_64x64x32_k2", [208, 1, 1]),  # unaligned, a partial stage: two groups
     (1536, 1024, 1024, "gemm_f32_mfma_64x64x32", [384, 1, 1]),  # 256 < tiles < 384: one group
     (512, 512, 512, "gemm_f32_direct_lds_32x32x32_w4", [256, 1, 1]),  # one launch, four waves split K via LDS
     (384, 384, 516, "gemm_f32_direct_lds_32x32x32_w4", [144, 1, 1]),  # ragged last slice
@@ -216,7 +217,8 @@ def test_gemm_launch_plans(m, n, k, kernel, grid):
     # is predicted 5% slower (K < 512 keeps the smaller tile); with at most
     # one 64x64 tile per CU, products of at most 32 rows as direct-load 32x32
     # tiles split over K, else 64x64 tiles with
-    # two K groups (four for K >= 768),
+    # two K groups (four for K >= 768, and for unaligned rows from K = 512
+    # when four groups split K's whole stages evenly, at most two k left),
     # and at most half the CUs' worth of
     # tiles either direct-load 32x32 tiles (aligned, moderate K) or split K.
     launch = describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
