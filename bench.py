@@ -728,10 +728,9 @@ def summarize_mfma(directory):
         gui = np.median(v["GRBM_GUI_ACTIVE"]) / XCDS
         if busy <= 0:
             continue
-        flag = " (saturated)" if busy >= 2.0 ** 31 else ""
         ghz = f"{np.median(v['_ghz']):.3f}" if v.get("_ghz") else "-"
         lines.append(f"| {key[0]} | {key[3]} | {key[1]} | {key[2]} | {len(v['GRBM_GUI_ACTIVE'])} | {gui:.0f} | "
-                     f"{busy:.4g}{flag} | {100.0 * busy / (gui * SIMDS):.1f}% | {ghz} |")
+                     f"{busy:.4g} | {100.0 * busy / (gui * SIMDS):.1f}% | {ghz} |")
     return "\n".join(lines)
 
 
