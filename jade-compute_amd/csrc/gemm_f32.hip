@@ -334,7 +334,7 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // the same bits. `nk` whole stages from kbegin; `t` is the thread's index in
 // its 256-thread group (every group of a workgroup runs the same number of
 // stages, so the barriers match).
-template <int TM, int TN, bool BUF = false>
+template <int TM, int TN, bool BUF = false, int QA = -1, int QB = 2>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
                                   int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
                                   f32x16 (&acc)[TM][TN], int M = 0) {
@@ -364,15 +364,18 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 const float *cur = smem + u * T::kStageS;
                 const bool more = k + 1 < nk;  // block-uniform
                 // Interior tiles: the next stage's A loads go out at the top
-                // of this stage, its B loads after the third quarter's operand
-                // reads.
+                // of this stage (QA < 0) or after quarter QA's operand reads,
+                // its B loads after quarter QB's.
                 auto spread = [&](int q) {
-                    if (more && q == 2)
+                    if (more && q == QA)
+                        issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
+                                                        lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 0);
+                    if (more && q == QB)
                         issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
                                                         lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 1);
                 };
                 if (BUF && more) issue(kbegin + (k + 1) * kBK, 1 - u);
-                if (!BUF && more)
+                if (!BUF && QA < 0 && more)
                     issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
                                                     lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 0);
                 // Raised wave priority while this wave has matrix work, so the
@@ -872,8 +875,17 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     // guarded, register-staged path.
     const bool whole = kmain - kfirst == KG * nk * kBK;
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && whole;
+    // Where the interior loop issues the next stage's two load parts (QA,
+    // QB) was measured per group count: four groups after quarters 1 and 3
+    // (1024^3 19.79 -> 19.54 us, 768^3 15.52 -> 15.38); one group of 64x64
+    // tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1, 1536x2048x1024 65.2
+    // -> 57.2, 3000x3000x3072 490 -> 450; grids of exactly two tiles per CU
+    // 0.6-0.9% slower); two groups and larger tiles A at the top, B after
+    // quarter 2. The same MFMAs in the same order: the bits do not change.
+    constexpr bool kOne64 = KG == 1 && TM * TN == 1;
+    constexpr int kQA = KG == 4 ? 1 : (kOne64 ? 0 : -1), kQB = KG == 4 ? 3 : (kOne64 ? 1 : 2);
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
-        k_loop_dma<TM, TN>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
+        k_loop_dma<TM, TN, false, kQA, kQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     // Edge tiles of aligned shapes, and every tile of an unaligned shape, with
     // whole stages: the same loop through range-checked buffer loads
     // (operands whose 32-bit offsets, with a tile of rows past M, stay below
