@@ -876,14 +876,19 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     const bool whole = kmain - kfirst == KG * nk * kBK;
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && whole;
     // Where the interior loop issues the next stage's two load parts (QA,
-    // QB) was measured per group count: four groups after quarters 1 and 3
-    // (1024^3 19.79 -> 19.54 us, 768^3 15.52 -> 15.38); one group of 64x64
-    // tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1, 1536x2048x1024 65.2
-    // -> 57.2, 3000x3000x3072 490 -> 450; grids of exactly two tiles per CU
-    // 0.6-0.9% slower); two groups and larger tiles A at the top, B after
-    // quarter 2. The same MFMAs in the same order: the bits do not change.
-    constexpr bool kOne64 = KG == 1 && TM * TN == 1;
-    constexpr int kQA = KG == 4 ? 1 : (kOne64 ? 0 : -1), kQB = KG == 4 ? 3 : (kOne64 ? 1 : 2);
+    // QB) was measured per tile and group count: four groups after quarters
+    // 1 and 3 (1024^3 19.79 -> 19.54 us, 768^3 15.52 -> 15.38); one group of
+    // 64x64 tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1,
+    // 1536x2048x1024 65.2 -> 57.2, 3000x3000x3072 490 -> 450; grids of
+    // exactly two tiles per CU 0.6-0.9% slower); 128x64 tiles after quarters
+    // 1 and 3 (3072x2048x1024 128.9 -> 102.4, 2304^3 261.7 -> 221.7,
+    // 1024x6144x512 67.5 -> 55.2, others within 0.1%); two groups and
+    // 128x128 tiles A at the top, B after quarter 2 (each alternative tried
+    // was 0.2-1.4% slower there). The same MFMAs in the same order: the bits
+    // do not change.
+    constexpr bool kOne64 = KG == 1 && TM * TN == 1, k128x64 = KG == 1 && TM * TN == 2;
+    constexpr int kQA = KG == 4 || k128x64 ? 1 : (kOne64 ? 0 : -1);
+    constexpr int kQB = KG == 4 || k128x64 ? 3 : (kOne64 ? 1 : 2);
     if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN, false, kQA, kQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     // Edge tiles of aligned shapes, and every tile of an unaligned shape, with
