@@ -1033,14 +1033,15 @@ struct Shape {
 };
 constexpr int kStage = Shape<2>::kStage;  // the LDS stage of either tile fits this one
 
-// Waves 0-3 load B for G, waves 4-7 B for U; all eight load A.
-template <int TM>
+// Waves 0-3 load B for G, waves 4-7 B for U; all eight load A. PART 0 issues
+// only the A loads, PART 1 only the B loads, -1 both.
+template <int TM, int PART = -1>
 __device__ inline void issue_stage(const float *__restrict__ A, const float *__restrict__ B, int N, int K, int m0,
                                    int n0, int k0, uint32_t stage_lds, int wave, int lane) {
     using S = Shape<TM>;
     const float *abase = A + size_t(m0) * K + k0;
 #pragma unroll
-    for (int i = 0; i < S::kAInst; ++i) {  // eight 128-byte A rows per 1 KiB load
+    for (int i = 0; i < (PART == 1 ? 0 : S::kAInst); ++i) {  // eight 128-byte A rows per 1 KiB load
         const int inst = wave * S::kAInst + i;
         const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
         lds_dma16(abase, uint32_t((row * K + 4 * j) * 4), stage_lds + inst * 1024);
@@ -1049,7 +1050,7 @@ __device__ inline void issue_stage(const float *__restrict__ A, const float *__r
     const uint32_t sb = stage_lds + (S::Tl::kAStageS + (wave >> 2) * S::Tl::kBStageS) * 4;
     constexpr int kChunks = S::Tl::kBN / 4, kRowsPer = 64 / kChunks;
 #pragma unroll
-    for (int i = 0; i < S::kBInst; ++i) {  // four 256-byte B rows per 1 KiB load
+    for (int i = 0; i < (PART == 0 ? 0 : S::kBInst); ++i) {  // four 256-byte B rows per 1 KiB load
         const int inst = (wave & 3) * S::kBInst + i;
         const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
         lds_dma16(bbase, uint32_t((row * N + 4 * j) * 4), sb + inst * 1024);
@@ -1089,14 +1090,20 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
             const int k = kt + uu, u = uu & 1;
             if (k < nk) {
                 const float *cur = smem + u * S::kStage;
-                if (k + 1 < nk)
-                    issue_stage<TM>(A, B, N, K, m0, n0, (k + 1) * kBK, lds0 + uint32_t((1 - u) * S::kStage * 4), wave,
-                                    lane);
+                const bool more = k + 1 < nk;
+                const uint32_t nxt = lds0 + uint32_t((1 - u) * S::kStage * 4);
+                auto spread = [&](int q) {
+                    if (more && q == 2) issue_stage<TM, 1>(A, B, N, K, m0, n0, (k + 1) * kBK, nxt, wave, lane);
+                };
+                // The next stage's A loads at the top of this stage, its B loads
+                // after the third quarter's operand reads (against all of them
+                // at the top: MLP block 520.4 -> 515.3 us).
+                if (more) issue_stage<TM, 0>(A, B, N, K, m0, n0, (k + 1) * kBK, nxt, wave, lane);
                 __builtin_amdgcn_s_setprio(1);
                 if (uu == 0)
-                    mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
+                    mma_stage_swz<TM, 1, true>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part, spread);
                 else
-                    mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part);
+                    mma_stage_swz<TM, 1, false>(cur, cur + Tl::kAStageS + group * Tl::kBStageS, wm, wn, lane, part, spread);
                 if (uu == FOLD - 1) {
 #pragma unroll
                     for (int i = 0; i < TM; ++i) acc[i][0] += part[i][0];
