@@ -57,6 +57,9 @@ constexpr int kThreads = 256;
 constexpr int kMaxTail = 2;
 constexpr int kLDA = kBK + 4;  // LDS row stride of an A stage (floats)
 constexpr uint32_t kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data format
+// A buffer-load offset past every buffer these kernels read (each below
+// 2 GiB): the range check returns zero without touching memory.
+constexpr uint32_t kDeadOffset = 0x80000000u;
 
 template <int TM, int TN>
 struct Tile {
@@ -138,18 +141,22 @@ __device__ inline void issue_stage_dma_part(const float *__restrict__ A, const f
 // through 16-byte buffer loads into LDS (buffer_load_dwordx4 ... lds) at
 // 4-byte-aligned offsets, whose range check returns zero past the end of A
 // (rows past M) and of B, so no bounds branch is needed. B runs past N read
-// the next row's first columns, which feed only unstored outputs. Whole
-// stages only (k stays below K). `ra` and `rb` cover A and B.
-template <int TM, int TN>
+// the next row's first columns, which feed only unstored outputs. `ra` and
+// `rb` cover A and B. MASK: k at or past `kend` (a partial last stage, or a
+// stage past the K range) reads zero, its A runs and B rows aimed at
+// kDeadOffset; with K % 4 == 0 an A run lies wholly below kend or wholly at
+// or past it. Without MASK the stage must lie below K.
+template <int TM, int TN, bool MASK = false>
 __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int N, int K, int m0,
-                                       int n0, int k0, float *stage, int t) {
+                                       int n0, int k0, float *stage, int t, int kend = 0) {
     using T = Tile<TM, TN>;
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
 #pragma unroll
     for (int i = 0; i < T::kAInst; ++i) {
         const int inst = wave * T::kAInst + i;
         const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
-        const uint32_t off = (uint32_t(m0 + row) * uint32_t(K) + uint32_t(k0 + 4 * j)) * 4u;
+        const uint32_t off =
+            !MASK || k0 + 4 * j < kend ? (uint32_t(m0 + row) * uint32_t(K) + uint32_t(k0 + 4 * j)) * 4u : kDeadOffset;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void *)(stage + inst * 256), 16,
                                                  int(off), 0, 0, 0);
     }
@@ -159,7 +166,8 @@ __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffe
     for (int i = 0; i < T::kBInst; ++i) {
         const int inst = wave * T::kBInst + i;
         const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
-        const uint32_t off = (uint32_t(k0 + row) * uint32_t(N) + uint32_t(n0 + 4 * j)) * 4u;
+        const uint32_t off =
+            !MASK || k0 + row < kend ? (uint32_t(k0 + row) * uint32_t(N) + uint32_t(n0 + 4 * j)) * 4u : kDeadOffset;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (__attribute__((address_space(3))) void *)(bstage + inst * 256),
                                                  16, int(off), 0, 0, 0);
     }
@@ -334,10 +342,10 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // the same bits. `nk` whole stages from kbegin; `t` is the thread's index in
 // its 256-thread group (every group of a workgroup runs the same number of
 // stages, so the barriers match).
-template <int TM, int TN, bool BUF = false, int QA = -1, int QB = 2>
+template <int TM, int TN, bool BUF = false, int QA = -1, int QB = 2, bool MASKED = false>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
                                   int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
-                                  f32x16 (&acc)[TM][TN], int M = 0) {
+                                  f32x16 (&acc)[TM][TN], int M = 0, int kend = 0) {
     using T = Tile<TM, TN>;
     const uint32_t lds0 = lds_address(smem);
     // BUF: edge tiles, through range-checked buffer loads over A and B.
@@ -347,7 +355,10 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
         const_cast<float *>(B), 0, BUF ? int(uint32_t(K) * uint32_t(N) * 4u) : 0, int(kBufferWord3));
     auto issue = [&](int k0, int buf) {
         if constexpr (BUF)
-            issue_stage_buf<TM, TN>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t);
+            if (!MASKED || k0 + kBK <= kend)  // block-uniform: a whole stage inside the K range
+                issue_stage_buf<TM, TN>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t);
+            else
+                issue_stage_buf<TM, TN, MASKED>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t, kend);
         else
             issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, k0, lds0 + uint32_t(buf * T::kStageS * 4), t);
     };
@@ -741,7 +752,10 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 // kUnalignedBuf: unaligned rows (no 16-byte-aligned loads) through buffer
 // loads, for 64x64 and 128x64 tiles over operands below 2 GiB each: into LDS
 // directly over whole stages, else staged in registers.
-enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2, kUnalignedBuf = 3 };
+// kBufAll: K ranges with a partial stage (K % 4 == 0, K >= 256, operands
+// whose 32-bit offsets fit): every tile through the buffer-load LDS-direct
+// loop, the partial and empty stages masked to zero.
+enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2, kUnalignedBuf = 3, kBufAll = 4 };
 
 // LDS-direct loads address each lane's 16 bytes as a 32-bit byte offset from
 // a wave-uniform base, computed in int: (row * K + 4 * chunk) * 4 for A rows
@@ -889,7 +903,9 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     constexpr bool kOne64 = KG == 1 && TM * TN == 1, k128x64 = KG == 1 && TM * TN == 2;
     constexpr int kQA = KG == 4 || k128x64 ? 1 : (kOne64 ? 0 : -1);
     constexpr int kQB = KG == 4 || k128x64 ? 3 : (kOne64 ? 1 : 2);
-    if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
+    if (PATH == kBufAll)
+        k_loop_dma<TM, TN, true, -1, 2, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M, kend);
+    else if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN, false, kQA, kQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     // Edge tiles of aligned shapes, and every tile of an unaligned shape, with
     // whole stages: the same loop through range-checked buffer loads
@@ -1319,7 +1335,6 @@ struct Slice {
 // `live` false (a prefetch past the wave's last slice): buffer loads go to an
 // offset past any buffer of this kernel, which reads zero without touching
 // memory, so the kernel does not end waiting on loads nobody consumes.
-constexpr uint32_t kDeadOffset = 0x80000000u;
 //
 // WHOLE (K % 32 == 0, with BUFB): every row of every slice lies inside B, so
 // a B row's step is the load's scalar offset and costs no VALU add.
@@ -1590,12 +1605,12 @@ __global__ __launch_bounds__(64 * G) void gemm_f32_direct_lds(const float *__res
         for (int i = 0; i < 4; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 ra, (__attribute__((address_space(3))) void *)(dst + i * 1024), 16,
-                int(live ? aoff[i] + 4u * k0 : direct::kDeadOffset), 0, 0, 0);
+                int(live ? aoff[i] + 4u * k0 : kDeadOffset), 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 rb, (__attribute__((address_space(3))) void *)(dst + 4096 + i * 1024), 16,
-                int(live ? boff[i] + 4u * k0 * uint32_t(N) : direct::kDeadOffset), 0, 0, 0);
+                int(live ? boff[i] + 4u * k0 * uint32_t(N) : kDeadOffset), 0, 0, 0);
     };
 #pragma unroll
     for (int j = 0; j < kRing; ++j) issue(j, j);
@@ -2040,8 +2055,22 @@ Plan plan_tiles(uint32_t m, uint32_t n, uint32_t k) {
 
 // The 4-wave kernel's load path for a launch: LDS-direct for every tile when
 // all are interior, aligned and within the 32-bit offsets; a per-tile choice
-// when only some are interior; register-staged otherwise.
+// when only some are interior; register-staged otherwise. K ranges with a
+// partial stage (K a multiple of 4, at least kBufAllMinK) take the masked
+// buffer-load loop for every tile instead of the register-staged one.
+// Measured against it (us): 3000^3 535.0 -> 484.3, 1000^3 23.37 -> 21.58,
+// 2000x2000x1000 78.1 -> 73.1, 2500^3 338.5 -> 321.4, 1000x776x548 15.04 ->
+// 14.25, 1000x1000x300 10.14 -> 9.77; at K = 100 it lost (6.05 -> 6.18).
+constexpr uint32_t kBufAllMinK = 256;
 Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int tm, int tn, int kg) {
+    {
+        const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
+        const bool whole = chunk % (kBK * kg) == 0 && last % (kBK * kg) == 0;
+        if (!whole && k % 4 == 0 && k >= kBufAllMinK &&
+            (uint64_t(m) + 64u * tm) * uint64_t(k) * 4u < (uint64_t(1) << 31) &&
+            (uint64_t(k) + 1) * uint64_t(n) * 4u + 64u * tn * 4u < (uint64_t(1) << 31))
+            return kBufAll;
+    }
     if (!vec)  // unaligned: no tile takes the LDS-direct loads
         return unaligned_buffers_fit(m, n, k) && tm * tn <= 2 ? kUnalignedBuf : kMixed;
     if (!dma_offsets_fit(uint32_t(64 * tm), uint32_t(64 * tn), k, n)) return kRegOnly;
@@ -2066,6 +2095,7 @@ bool tile_instantiated(int tm, int tn, int kg, Path path, bool vec) {
         case kRegOnly: return vec;
         case kUnalignedBuf: return !vec && tm * tn <= 2;
         case kMixed: return vec || kg <= 2;
+        case kBufAll: return true;
     }
     return false;
 }
@@ -2156,6 +2186,9 @@ hipError_t launch_tile(hipStream_t stream, const Route &r, const float *a, const
             if constexpr (TM * TN <= 2)
                 return launch_unaligned<TM, TN, KG, kUnalignedBuf>(stream, r, grid, block, a, b, out, m, n, k, pair);
             break;
+        case kBufAll:
+            if (r.vec) return launch_instance<TM, TN, KG, kBufAll, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
+            return launch_instance<TM, TN, KG, kBufAll, false>(stream, p, grid, block, a, b, out, m, n, k, pair);
         case kMixed:
             if (r.vec) return launch_instance<TM, TN, KG, kMixed, true>(stream, p, grid, block, a, b, out, m, n, k, pair);
             if constexpr (KG <= 2)

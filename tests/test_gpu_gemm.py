@@ -241,6 +241,28 @@ def test_unaligned_whole_stages_through_buffer_loads_into_lds(runtime, m, n, k, 
 
 
 @pytest.mark.parametrize("m,n,k,kernel", [
+    (1000, 1000, 1000, "gemm_f32_mfma_64x64x32_k4"),  # 31 stages and 8 k: the last group's last stage partial
+    (1000, 776, 548, "gemm_f32_mfma_64x64x32_k2"),
+    (2000, 1554, 1028, "gemm_f32_mfma_128x64x32"),  # N unaligned: B runs past N, K with 4 k in its last stage
+    (700, 1300, 292, "gemm_f32_mfma_64x64x32_k2"),
+    (200, 8, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),  # slices of 160 k: each slice's last group stage lies
+                                                          # in the next slice, whose B rows must read as zero
+    (1024, 512, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),
+])
+def test_partial_stages_through_masked_buffer_loads(runtime, m, n, k, kernel):
+    # K ranges with a partial stage (K % 4 == 0, K >= 256) load every tile's
+    # stages straight into LDS through buffer loads; k at or past the range's
+    # end is aimed past the buffers and reads zero.
+    launch = runtime.compile({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True}).launch
+    assert launch["kernel"] == kernel, launch
+    a = orc.values(m * k, 0xB9, 1.0)
+    b = orc.values(k * n, 0xC9, 1.0)
+    got = run_gemm(runtime, m, n, k, a, b, repeats=2)
+    rows = None if m * n * k <= 2e9 else (0, 256)
+    gate(got, m, n, k, a, b, rows=rows)
+
+
+@pytest.mark.parametrize("m,n,k,kernel", [
     (1024, 1024, 512, "gemm_f32_mfma_64x64x32_k2"),  # LDS-direct stages, 8 per group
     (1000, 777, 700, "gemm_f32_mfma_64x64x32_k2"),  # unaligned rows, K below the four-group threshold
     (130, 70, 100, "gemm_f32_mfma_64x64x32_k2"),  # 4 stages, the last one partial

@@ -9,8 +9,9 @@ map covers every output exactly once. The kernel's index formulas are
 restated with numpy over all lanes, waves, instructions and stages, so a
 launch that the fusion rule accepts cannot address memory outside the
 bindings or the 64 KiB of LDS it declares. The tile kernel's buffer loads
-into LDS over unaligned rows are checked the same way: every run that feeds
-a stored output holds its own row's elements of the K range."""
+into LDS over unaligned rows and over partial stages are checked the same
+way: every run that feeds a stored output holds its own row's elements of
+the K range, and k outside it reads zero."""
 import numpy as np
 import pytest
 
@@ -294,3 +295,60 @@ def test_unaligned_whole_stages_load_inside_their_rows(m, n, k):
         assert off.max() * 4 < 2 ** 32
         assert rows.max() < kmain
         assert (off[cols < n] < k * n).all()
+
+
+DEAD = 0x80000000  # kDeadOffset: past every buffer these kernels read
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 1000, 1000), (1000, 776, 548), (2000, 1554, 1028), (700, 1300, 292),
+                                   (200, 8, 1000), (1024, 512, 1000), (3000, 3000, 3000), (2500, 2500, 2500)])
+def test_partial_stages_mask_every_k_outside_the_range(m, n, k):
+    """K ranges with a partial stage run every tile through the masked
+    buffer loads into LDS: per K slice and group, the live A runs of a tile row
+    cover each k of the slice exactly once, every run at or past the group's
+    end is aimed past both buffers (kDeadOffset, zero from the range check)
+    and no live run or B row reaches past the slice, so a split product never
+    reads the next slice's rows. Slices come from the library's own launch
+    description."""
+    import jade_hip
+    launch = jade_hip.spec_describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
+    name = launch["kernel"]
+    assert name.startswith("gemm_f32_mfma_"), name
+    dims = name.split("_")[3]
+    bm, bn = int(dims.split("x")[0]), int(dims.split("x")[1])
+    last = name.split("_")[-1]
+    kg = int(last[1:]) if last.startswith("k") else 1
+    slices = launch["grid"][1]
+    kchunk = -(-(-(-k // slices)) // BK) * BK
+    assert -(-k // kchunk) == slices
+    assert k % 4 == 0 and (m + bm) * k * 4 < DEAD and (k + 1) * n * 4 + bn * 4 < DEAD
+    (a_row, a_col, _), (b_row, b_col, _) = tile_buf_loads(bm // 64, bn // 64)
+    a_row, a_col = a_row.ravel(), a_col.ravel()
+    b_row, b_col = b_row.ravel(), b_col.ravel()
+    partial = False
+    for z in range(slices):
+        kfirst, klast = z * kchunk, min(k, (z + 1) * kchunk)
+        nk = -(-(-(-(klast - kfirst) // BK)) // kg)
+        partial |= klast - kfirst != kg * nk * BK
+        cover = np.zeros((bm, klast - kfirst), dtype=np.int64)
+        for g in range(kg):
+            kbegin = kfirst + g * nk * BK
+            kend = min(klast, kbegin + nk * BK)
+            for s in range(nk):
+                k0 = kbegin + s * BK
+                ka = k0 + a_col
+                live = ka < kend
+                # A: live runs stay inside [kfirst, klast) and cover it once.
+                assert (ka[live] + 3 < klast).all() and (ka[live] >= kfirst).all()
+                for r, c in zip(a_row[live], ka[live]):
+                    cover[r, c - kfirst:c - kfirst + 4] += 1
+                off = np.where(live, (a_row.astype(np.int64) * k + ka) * 4, DEAD)
+                assert (off[~live] == DEAD).all() and off[live].max(initial=0) < DEAD
+                # B: live rows below the slice's end, dead rows past both buffers.
+                kb = k0 + b_row
+                live_b = kb < kend
+                assert (kb[live_b] < klast).all()
+                offb = np.where(live_b, (kb.astype(np.int64) * n + b_col) * 4, DEAD)
+                assert offb[live_b].max(initial=0) < DEAD and (offb[~live_b] == DEAD).all()
+        assert (cover == 1).all()
+    assert partial  # these shapes take the masked loop
