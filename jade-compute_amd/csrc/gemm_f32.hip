@@ -144,8 +144,10 @@ __device__ inline void issue_stage_dma_part(const float *__restrict__ A, const f
 // the next row's first columns, which feed only unstored outputs. `ra` and
 // `rb` cover A and B. MASK: k at or past `kend` (a partial last stage, or a
 // stage past the K range) reads zero, its A runs and B rows aimed at
-// kDeadOffset; with K % 4 == 0 an A run lies wholly below kend or wholly at
-// or past it. Without MASK the stage must lie below K.
+// kDeadOffset. With K % 4 == 0 an A run lies wholly below kend or wholly at
+// or past it; otherwise a run that straddles kend is loaded whole and its k
+// past kend zeroed in LDS afterwards (k_loop_dma). Without MASK the stage
+// must lie below K.
 template <int TM, int TN, bool MASK = false>
 __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int N, int K, int m0,
                                        int n0, int k0, float *stage, int t, int kend = 0) {
@@ -362,8 +364,29 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
         else
             issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, k0, lds0 + uint32_t(buf * T::kStageS * 4), t);
     };
+    // MASKED with unaligned rows (K % 4 != 0): an A run that straddles kend
+    // was loaded whole; once this wave's loads have landed it zeroes the
+    // run's k at or past kend in LDS, before the barrier publishes the stage.
+    auto fix = [&](int k0, int buf) {
+        if constexpr (MASKED) {
+            if (K % 4 != 0 && k0 + kBK > kend) {  // block-uniform
+                float *stage = smem + buf * T::kStageS;
+                const int wave = t >> 6;
+#pragma unroll
+                for (int i = 0; i < T::kAInst; ++i) {
+                    const int inst = wave * T::kAInst + i;
+                    const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
+                    const int ka = k0 + 4 * j;
+#pragma unroll
+                    for (int e = 1; e < 4; ++e)
+                        if (ka < kend && ka + e >= kend) stage[inst * 256 + lane * 4 + e] = 0.f;
+                }
+            }
+        }
+    };
     issue(kbegin, 0);
     drain_vmem();
+    fix(kbegin, 0);
     __syncthreads();
     // Partial sums run over kFoldStages stages before each fold into acc.
     f32x16 part[TM][TN];
@@ -412,6 +435,7 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 }
                 __builtin_amdgcn_s_setprio(0);
                 drain_vmem();
+                if (more) fix(kbegin + (k + 1) * kBK, 1 - u);
                 __syncthreads();
             }
         }
@@ -752,7 +776,7 @@ __device__ inline void k_loop_unaligned(const float *__restrict__ A, const float
 // kUnalignedBuf: unaligned rows (no 16-byte-aligned loads) through buffer
 // loads, for 64x64 and 128x64 tiles over operands below 2 GiB each: into LDS
 // directly over whole stages, else staged in registers.
-// kBufAll: K ranges with a partial stage (K % 4 == 0, K >= 256, operands
+// kBufAll: K ranges with a partial stage (tile_path gives the rule; operands
 // whose 32-bit offsets fit): every tile through the buffer-load LDS-direct
 // loop, the partial and empty stages masked to zero.
 enum Path { kMixed = 0, kDmaOnly = 1, kRegOnly = 2, kUnalignedBuf = 3, kBufAll = 4 };
@@ -2056,17 +2080,23 @@ Plan plan_tiles(uint32_t m, uint32_t n, uint32_t k) {
 // The 4-wave kernel's load path for a launch: LDS-direct for every tile when
 // all are interior, aligned and within the 32-bit offsets; a per-tile choice
 // when only some are interior; register-staged otherwise. K ranges with a
-// partial stage (K a multiple of 4, at least kBufAllMinK) take the masked
-// buffer-load loop for every tile instead of the register-staged one.
+// partial stage (K at least kBufAllMinK, and no epilogue tail) take the
+// masked buffer-load loop for every tile instead of the register-staged one.
 // Measured against it (us): 3000^3 535.0 -> 484.3, 1000^3 23.37 -> 21.58,
 // 2000x2000x1000 78.1 -> 73.1, 2500^3 338.5 -> 321.4, 1000x776x548 15.04 ->
 // 14.25, 1000x1000x300 10.14 -> 9.77; at K = 100 it lost (6.05 -> 6.18).
+// Unaligned K (a run straddling the range's end is zeroed past it in LDS):
+// 3000x3000x3001 535.4 -> 503.6, 1000x777x1027 25.48 -> 24.47,
+// 2048x2048x2047 145.5 -> 142.3, 4095x4097x4093 1300 -> 1273; with two K
+// groups it lost (1000x777x700 16.23 -> 16.71, 1000x777x300 9.31 -> 9.53),
+// so those keep the register-staged loop.
 constexpr uint32_t kBufAllMinK = 256;
+bool ktail_fits(const Plan &p, bool vec, int kg, uint32_t k);
 Path tile_path(const Plan &p, bool vec, uint32_t m, uint32_t n, uint32_t k, int tm, int tn, int kg) {
     {
         const uint32_t chunk = uint32_t(p.kchunk), last = k - (uint32_t(p.slices) - 1) * chunk;
         const bool whole = chunk % (kBK * kg) == 0 && last % (kBK * kg) == 0;
-        if (!whole && k % 4 == 0 && k >= kBufAllMinK &&
+        if (!whole && !ktail_fits(p, vec, kg, k) && k >= kBufAllMinK && (k % 4 == 0 || kg != 2) &&
             (uint64_t(m) + 64u * tm) * uint64_t(k) * 4u < (uint64_t(1) << 31) &&
             (uint64_t(k) + 1) * uint64_t(n) * 4u + 64u * tn * 4u < (uint64_t(1) << 31))
             return kBufAll;

@@ -160,6 +160,7 @@ def test_direct_tiles_over_unaligned_rows(runtime, m, n, k, waves):
 
 @pytest.mark.parametrize("m,n,k", [
     (1000, 777, 545),  # 64x64 tiles, two K groups, unaligned rows: the last stage runs 31 k past K
+    (1000, 777, 1027),  # four K groups, masked LDS-direct stages: row 4's last run straddles K, zeroed in LDS
     (200, 8, 999),     # K split into slices of 160: a slice's last stage runs into the next slice
     (500, 777, 513),   # direct-load 32x32 tiles over unaligned rows
 ])
@@ -245,6 +246,8 @@ def test_unaligned_whole_stages_through_buffer_loads_into_lds(runtime, m, n, k, 
     (1000, 776, 548, "gemm_f32_mfma_64x64x32_k2"),
     (2000, 1554, 1028, "gemm_f32_mfma_128x64x32"),  # N unaligned: B runs past N, K with 4 k in its last stage
     (700, 1300, 292, "gemm_f32_mfma_64x64x32_k2"),
+    (3000, 3001, 3001, "gemm_f32_mfma_64x64x32"),  # unaligned K: the last stage's straddling runs zeroed past K
+    (1000, 777, 1027, "gemm_f32_mfma_64x64x32_k4"),
     (200, 8, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),  # slices of 160 k: each slice's last group stage lies
                                                           # in the next slice, whose B rows must read as zero
     (1024, 512, 1000, "gemm_f32_mfma_64x64x32_splitk_k2"),

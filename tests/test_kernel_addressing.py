@@ -301,15 +301,17 @@ DEAD = 0x80000000  # kDeadOffset: past every buffer these kernels read
 
 
 @pytest.mark.parametrize("m,n,k", [(1000, 1000, 1000), (1000, 776, 548), (2000, 1554, 1028), (700, 1300, 292),
-                                   (200, 8, 1000), (1024, 512, 1000), (3000, 3000, 3000), (2500, 2500, 2500)])
+                                   (200, 8, 1000), (1024, 512, 1000), (3000, 3000, 3000), (2500, 2500, 2500),
+                                   (3000, 3001, 3001), (1000, 777, 1027), (2048, 2048, 2047)])
 def test_partial_stages_mask_every_k_outside_the_range(m, n, k):
     """K ranges with a partial stage run every tile through the masked
-    buffer loads into LDS: per K slice and group, the live A runs of a tile row
-    cover each k of the slice exactly once, every run at or past the group's
-    end is aimed past both buffers (kDeadOffset, zero from the range check)
-    and no live run or B row reaches past the slice, so a split product never
-    reads the next slice's rows. Slices come from the library's own launch
-    description."""
+    buffer loads into LDS: per K slice and group, the live A elements of a
+    tile row cover each k of the slice exactly once, every run that starts at
+    or past the group's end is aimed past both buffers (kDeadOffset, zero
+    from the range check), a run that straddles the end (unaligned K) has
+    exactly its k past the end zeroed in LDS, and no live B row reaches past
+    the slice, so a split product never reads the next slice's rows. Slices
+    come from the library's own launch description."""
     import jade_hip
     launch = jade_hip.spec_describe({"op": "gemm", "m": m, "n": n, "k": k, "tiled": True})["launch"]
     name = launch["kernel"]
@@ -321,7 +323,7 @@ def test_partial_stages_mask_every_k_outside_the_range(m, n, k):
     slices = launch["grid"][1]
     kchunk = -(-(-(-k // slices)) // BK) * BK
     assert -(-k // kchunk) == slices
-    assert k % 4 == 0 and (m + bm) * k * 4 < DEAD and (k + 1) * n * 4 + bn * 4 < DEAD
+    assert (m + bm) * k * 4 < DEAD and (k + 1) * n * 4 + bn * 4 < DEAD
     (a_row, a_col, _), (b_row, b_col, _) = tile_buf_loads(bm // 64, bn // 64)
     a_row, a_col = a_row.ravel(), a_col.ravel()
     b_row, b_col = b_row.ravel(), b_col.ravel()
@@ -338,10 +340,15 @@ def test_partial_stages_mask_every_k_outside_the_range(m, n, k):
                 k0 = kbegin + s * BK
                 ka = k0 + a_col
                 live = ka < kend
-                # A: live runs stay inside [kfirst, klast) and cover it once.
-                assert (ka[live] + 3 < klast).all() and (ka[live] >= kfirst).all()
+                # A: live runs start inside [kfirst, klast); their elements
+                # below kend cover it once, the rest (a straddling run's tail,
+                # K % 4 != 0 only) is what k_loop_dma zeroes in LDS.
+                assert (ka[live] >= kfirst).all()
+                straddle = live & (ka + 3 >= kend)
+                assert k % 4 != 0 or not straddle.any()
                 for r, c in zip(a_row[live], ka[live]):
-                    cover[r, c - kfirst:c - kfirst + 4] += 1
+                    hi = min(c + 4, kend)
+                    cover[r, c - kfirst:hi - kfirst] += 1
                 off = np.where(live, (a_row.astype(np.int64) * k + ka) * 4, DEAD)
                 assert (off[~live] == DEAD).all() and off[live].max(initial=0) < DEAD
                 # B: live rows below the slice's end, dead rows past both buffers.
