@@ -148,13 +148,13 @@ __device__ inline void issue_stage_dma_part(const float *__restrict__ A, const f
 // or past it; otherwise a run that straddles kend is loaded whole and its k
 // past kend zeroed in LDS afterwards (k_loop_dma). Without MASK the stage
 // must lie below K.
-template <int TM, int TN, bool MASK = false>
+template <int TM, int TN, bool MASK = false, int PART = -1>
 __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffer_rsrc_t rb, int N, int K, int m0,
                                        int n0, int k0, float *stage, int t, int kend = 0) {
     using T = Tile<TM, TN>;
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
 #pragma unroll
-    for (int i = 0; i < T::kAInst; ++i) {
+    for (int i = 0; i < (PART == 1 ? 0 : T::kAInst); ++i) {
         const int inst = wave * T::kAInst + i;
         const int row = inst * 8 + (lane >> 3), j = (lane & 7) ^ swz_a(row);
         const uint32_t off =
@@ -165,7 +165,7 @@ __device__ inline void issue_stage_buf(__amdgpu_buffer_rsrc_t ra, __amdgpu_buffe
     constexpr int kChunks = T::kBN / 4, kRowsPer = 64 / kChunks;
     float *bstage = stage + T::kAStageS;
 #pragma unroll
-    for (int i = 0; i < T::kBInst; ++i) {
+    for (int i = 0; i < (PART == 0 ? 0 : T::kBInst); ++i) {
         const int inst = wave * T::kBInst + i;
         const int row = inst * kRowsPer + lane / kChunks, j = (lane % kChunks) ^ swz_b(row);
         const uint32_t off =
@@ -344,7 +344,10 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
 // the same bits. `nk` whole stages from kbegin; `t` is the thread's index in
 // its 256-thread group (every group of a workgroup runs the same number of
 // stages, so the barriers match).
-template <int TM, int TN, bool BUF = false, int QA = -1, int QB = 2, bool MASKED = false>
+// BUF: BQB < 0 issues the next stage whole at the top of the current one;
+// else its A loads at the top (BQA < 0) or after quarter BQA's operand
+// reads, and its B loads after quarter BQB's.
+template <int TM, int TN, bool BUF = false, int QA = -1, int QB = 2, bool MASKED = false, int BQA = -1, int BQB = -1>
 __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__restrict__ B, float *smem, int N,
                                   int K, int kbegin, int nk, int m0, int n0, int wm, int wn, int lane, int t,
                                   f32x16 (&acc)[TM][TN], int M = 0, int kend = 0) {
@@ -363,6 +366,13 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 issue_stage_buf<TM, TN, MASKED>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t, kend);
         else
             issue_stage_dma<TM, TN>(A, B, N, K, m0, n0, k0, lds0 + uint32_t(buf * T::kStageS * 4), t);
+    };
+    auto issue_buf_part = [&](int k0, int buf, auto part) {
+        constexpr int kPart = decltype(part)::value;
+        if (!MASKED || k0 + kBK <= kend)
+            issue_stage_buf<TM, TN, false, kPart>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t);
+        else
+            issue_stage_buf<TM, TN, MASKED, kPart>(ra, rb, N, K, m0, n0, k0, smem + buf * T::kStageS, t, kend);
     };
     // MASKED with unaligned rows (K % 4 != 0): an A run that straddles kend
     // was loaded whole; once this wave's loads have landed it zeroes the
@@ -401,6 +411,13 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 // of this stage (QA < 0) or after quarter QA's operand reads,
                 // its B loads after quarter QB's.
                 auto spread = [&](int q) {
+                    if constexpr (BUF) {
+                        if (BQB >= 0 && more && q == BQA)
+                            issue_buf_part(kbegin + (k + 1) * kBK, 1 - u, std::integral_constant<int, 0>{});
+                        if (BQB >= 0 && more && q == BQB)
+                            issue_buf_part(kbegin + (k + 1) * kBK, 1 - u, std::integral_constant<int, 1>{});
+                        return;
+                    }
                     if (more && q == QA)
                         issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
                                                         lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 0);
@@ -408,7 +425,9 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                         issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
                                                         lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 1);
                 };
-                if (BUF && more) issue(kbegin + (k + 1) * kBK, 1 - u);
+                if (BUF && BQB < 0 && more) issue(kbegin + (k + 1) * kBK, 1 - u);
+                if (BUF && BQB >= 0 && BQA < 0 && more)
+                    issue_buf_part(kbegin + (k + 1) * kBK, 1 - u, std::integral_constant<int, 0>{});
                 if (!BUF && QA < 0 && more)
                     issue_stage_dma_part<TM, TN, 2>(A, B, N, K, m0, n0, kbegin + (k + 1) * kBK,
                                                     lds0 + uint32_t((1 - u) * T::kStageS * 4), t, 0);
@@ -416,7 +435,7 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                 // SIMD's arbiter favours it over the co-resident workgroup's
                 // loads and folds (measured +1-2% at 4096^3).
                 __builtin_amdgcn_s_setprio(1);
-                if constexpr (BUF) {
+                if constexpr (BUF && BQB < 0) {
                     if (uu == 0)
                         mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part);
                     else
@@ -927,8 +946,14 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     constexpr bool kOne64 = KG == 1 && TM * TN == 1, k128x64 = KG == 1 && TM * TN == 2;
     constexpr int kQA = KG == 4 || k128x64 ? 1 : (kOne64 ? 0 : -1);
     constexpr int kQB = KG == 4 || k128x64 ? 3 : (kOne64 ? 1 : 2);
+    // The buffer-load loop (edge tiles, unaligned rows, partial stages)
+    // issues the next stage whole at the top of the current one, except with
+    // two K groups and for 128x128 tiles, where A at the top and B after
+    // quarter 2 measured faster (1000x832x512 12.38 -> 12.26 us, 2500^3
+    // 322.5 -> 314.7); elsewhere that split was 0.5-6% slower.
+    constexpr int kBufQB = KG == 2 || TM * TN == 4 ? 2 : -1;
     if (PATH == kBufAll)
-        k_loop_dma<TM, TN, true, -1, 2, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M, kend);
+        k_loop_dma<TM, TN, true, -1, 2, true, -1, kBufQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M, kend);
     else if (PATH == kDmaOnly || (PATH == kMixed && VEC && interior))
         k_loop_dma<TM, TN, false, kQA, kQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc);
     // Edge tiles of aligned shapes, and every tile of an unaligned shape, with
@@ -945,7 +970,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     else if (((PATH == kMixed && VEC) || PATH == kUnalignedBuf) && whole &&
              (uint64_t(M) + T::kBM) * uint64_t(K) * 4u < (uint64_t(1) << 31) &&
              (uint64_t(K) + 1) * uint64_t(N) * 4u + T::kBN * 4u < (uint64_t(1) << 31))
-        k_loop_dma<TM, TN, true>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);
+        k_loop_dma<TM, TN, true, -1, 2, false, -1, kBufQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M);
     else if (!VEC && TM * TN <= 2)  // the 128x128 tile would spill with two register stages
         k_loop_unaligned<TM, TN, PATH == kUnalignedBuf, KG == 2, TM * TN == 2 || KG == 2, TM * TN == 1 && KG != 2>(
             A, B, gsmem, M, N, K, kbegin, kend, nk, m0, n0, wm, wn, lane, t, acc);
