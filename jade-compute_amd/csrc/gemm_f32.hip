@@ -17,10 +17,12 @@
 //    128x64) plus a partial round of 128x128 or 64x64 tiles.
 //  * K advances 32 per stage. Stages are double-buffered in LDS and filled by
 //    LDS-direct loads: global loads for interior tiles, range-checked buffer
-//    loads for edge tiles and for unaligned rows over whole stages. K ranges
-//    with a partial stage, and operands too long for 32-bit offsets, take a
-//    register prefetch (unaligned 64x64 and 128x64 tiles keep two stages in
-//    registers, loaded through buffer instructions). One barrier per stage.
+//    loads for edge tiles, for unaligned rows over whole stages and, masked
+//    past the K range, for K ranges with a partial stage (K of at least 256;
+//    not unaligned K with two K groups). The rest, and operands too long for
+//    32-bit offsets, take a register prefetch (unaligned 64x64 and 128x64
+//    tiles keep two stages in registers, loaded through buffer
+//    instructions). One barrier per stage.
 //  * The MFMA K=2 operand split is permuted: lanes 0-31 take k in [0,16) and
 //    lanes 32-63 take k in [16,32) of a stage, so an A operand run is 16
 //    contiguous floats per lane (ds_read_b128) while B stays ds_read_b32 with
