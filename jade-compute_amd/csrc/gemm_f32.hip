@@ -935,19 +935,20 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     const bool whole = kmain - kfirst == KG * nk * kBK;
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && whole;
     // Where the interior loop issues the next stage's two load parts (QA,
-    // QB) was measured per tile and group count: four groups after quarters
-    // 1 and 3 (1024^3 19.79 -> 19.54 us, 768^3 15.52 -> 15.38); one group of
-    // 64x64 tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1,
+    // QB) was measured per tile and group count (A at the top, B after
+    // quarter 2 before): two and four groups after quarters 1 and 2 (1024^3
+    // 19.79 -> 19.49 us, 1024x1024x2048 37.0 -> 34.9, 1024x1024x4096 69.7 ->
+    // 65.9, 768x768x1024 19.78 -> 19.26, 1024x832x512 11.47 -> 11.39); one
+    // group of 64x64 tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1,
     // 1536x2048x1024 65.2 -> 57.2, 3000x3000x3072 490 -> 450; grids of
     // exactly two tiles per CU 0.6-0.9% slower); 128x64 tiles after quarters
     // 1 and 3 (3072x2048x1024 128.9 -> 102.4, 2304^3 261.7 -> 221.7,
-    // 1024x6144x512 67.5 -> 55.2, others within 0.1%); two groups and
-    // 128x128 tiles A at the top, B after quarter 2 (each alternative tried
-    // was 0.2-1.4% slower there). The same MFMAs in the same order: the bits
-    // do not change.
+    // 1024x6144x512 67.5 -> 55.2, others within 0.1%); 128x128 tiles keep A
+    // at the top and B after quarter 2 (each alternative tried was 0.2-0.4%
+    // slower). The same MFMAs in the same order: the bits do not change.
     constexpr bool kOne64 = KG == 1 && TM * TN == 1, k128x64 = KG == 1 && TM * TN == 2;
-    constexpr int kQA = KG == 4 || k128x64 ? 1 : (kOne64 ? 0 : -1);
-    constexpr int kQB = KG == 4 || k128x64 ? 3 : (kOne64 ? 1 : 2);
+    constexpr int kQA = KG > 1 || k128x64 ? 1 : (kOne64 ? 0 : -1);
+    constexpr int kQB = KG > 1 ? 2 : (k128x64 ? 3 : (kOne64 ? 1 : 2));
     // The buffer-load loop (edge tiles, unaligned rows, partial stages)
     // issues the next stage whole at the top of the current one, except with
     // two K groups and for 128x128 tiles, where A at the top and B after
