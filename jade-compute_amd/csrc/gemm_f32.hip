@@ -942,13 +942,13 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     // group of 64x64 tiles after quarters 0 and 1 (1536^3 83.2 -> 78.1,
     // 1536x2048x1024 65.2 -> 57.2, 3000x3000x3072 490 -> 450; grids of
     // exactly two tiles per CU 0.6-0.9% slower); 128x64 tiles after quarters
-    // 1 and 3 (3072x2048x1024 128.9 -> 102.4, 2304^3 261.7 -> 221.7,
-    // 1024x6144x512 67.5 -> 55.2, others within 0.1%); 128x128 tiles keep A
+    // 1 and 2 as well (3072x2048x1024 128.9 -> 100.2, 2304^3 261.7 -> 216.3,
+    // 1024x6144x512 67.5 -> 53.3, others within 0.5%); 128x128 tiles keep A
     // at the top and B after quarter 2 (each alternative tried was 0.2-0.4%
     // slower). The same MFMAs in the same order: the bits do not change.
     constexpr bool kOne64 = KG == 1 && TM * TN == 1, k128x64 = KG == 1 && TM * TN == 2;
     constexpr int kQA = KG > 1 || k128x64 ? 1 : (kOne64 ? 0 : -1);
-    constexpr int kQB = KG > 1 ? 2 : (k128x64 ? 3 : (kOne64 ? 1 : 2));
+    constexpr int kQB = KG > 1 || k128x64 ? 2 : (kOne64 ? 1 : 2);
     // The buffer-load loop (edge tiles, unaligned rows, partial stages)
     // issues the next stage whole at the top of the current one, except with
     // two K groups and for 128x128 tiles, where A at the top and B after
