@@ -931,6 +931,7 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     // Interior tiles with 16-byte rows stream through LDS-direct loads; edge
     // tiles and unaligned shapes over whole stages take the same loop through
     // buffer loads; K ranges that are not KG x nk whole stages take the
+    // masked form of that loop (PATH kBufAll, chosen by the host) or the
     // guarded, register-staged path.
     const bool whole = kmain - kfirst == KG * nk * kBK;
     const bool interior = m0 + T::kBM <= M && n0 + T::kBN <= N && whole;
