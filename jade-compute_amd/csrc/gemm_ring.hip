@@ -54,8 +54,10 @@ namespace {
 // instead of issued back to back (the waves then waited on the LDS pipe four
 // times as long as the library's kernel), 147.4 with four waves and 149.3 with
 // eight; runs of eight stages instead of four before each fold (kFoldRun),
-// 149.4. Halving the barriers (a timing-only copy without the odd stages'
-// barriers) and folding the two waves of a SIMD at different stages (so one
+// 149.4; each load after the seventh of its eight MFMAs instead of the last,
+// 150.5 (identical bits; 4096x11008x4096 -0.7% time, 2048^3 -0.5%).
+// Halving the barriers (a timing-only copy without the odd stages' barriers)
+// and folding the two waves of a SIMD at different stages (so one
 // wave's MFMAs cover the other's fold) were measured and changed nothing.
 // Also measured and dropped: sixteen waves of 32x32 (four per SIMD), 1%
 // slower at every shape; 128x256 tiles of 16-deep stages (eight waves of
@@ -303,7 +305,11 @@ __global__ __launch_bounds__(512 / TM) __attribute__((amdgpu_waves_per_eu(3 - TM
                             read_part(rslot, rq, n, nxt);
                             __builtin_amdgcn_sched_barrier(0);
                         }
-                        if (n % 8 == 7) {
+                        // A load goes out after MFMA 6 of each eight, one
+                        // before the group's end: 4096^3 920.8 -> 913.5 us
+                        // against the group's last MFMA (after MFMA 5 917.4,
+                        // 4 917.8, 3 921.2, 0 919.5).
+                        if (n % 8 == 6) {
                             __builtin_amdgcn_sched_barrier(0);
                             issue_part((U + 3) % kDepth, q * (kMfmas / 8) + n / 8);
                             __builtin_amdgcn_sched_barrier(0);
