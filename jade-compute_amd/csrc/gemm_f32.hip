@@ -1166,7 +1166,9 @@ __device__ inline void tile(const float *__restrict__ A, const float *__restrict
                 };
                 // The next stage's A loads at the top of this stage, its B loads
                 // after the third quarter's operand reads (against all of them
-                // at the top: MLP block 520.4 -> 515.3 us).
+                // at the top: MLP block 520.4 -> 515.3 us; A after the second
+                // quarter's reads 538.3, after the first 541.7, A and B after
+                // the first and second 530.0, B after the fourth 517.7).
                 if (more) issue_stage<TM, 0>(A, B, N, K, m0, n0, (k + 1) * kBK, nxt, wave, lane);
                 __builtin_amdgcn_s_setprio(1);
                 if (uu == 0)

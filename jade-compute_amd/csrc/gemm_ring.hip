@@ -308,7 +308,9 @@ __global__ __launch_bounds__(512 / TM) __attribute__((amdgpu_waves_per_eu(3 - TM
                         // A load goes out after MFMA 6 of each eight, one
                         // before the group's end: 4096^3 920.8 -> 913.5 us
                         // against the group's last MFMA (after MFMA 5 917.4,
-                        // 4 917.8, 3 921.2, 0 919.5).
+                        // 4 917.8, 3 921.2, 0 919.5). Moving the operand
+                        // reads instead (one MFMA later, spread over the
+                        // quarter, or B rows first) changed nothing (0.2%).
                         if (n % 8 == 6) {
                             __builtin_amdgcn_sched_barrier(0);
                             issue_part((U + 3) % kDepth, q * (kMfmas / 8) + n / 8);
