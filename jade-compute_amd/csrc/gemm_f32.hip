@@ -287,9 +287,16 @@ __device__ inline void mma_stage(const float *stage, int wm, int wn, int lane, f
 struct NoHook {
     __device__ void operator()(int) const {}
 };
-// `hook(q)` runs after quarter q's operand reads are issued and before its
-// MFMAs (the LDS-direct loop issues a share of the next stage's loads there).
-template <int TM, int TN, bool ZERO = true, class Hook = NoHook>
+// `hook(q)` runs after quarter q's operand reads are issued (the LDS-direct
+// loop issues a share of the next stage's loads there): before the quarter's
+// MFMAs, or with LATE after its first two of four. The tile loops take LATE
+// for 64x64 wave tiles (us, the same bits: 1024^3 19.53 -> 19.47, 2048x1024x512
+// 20.45 -> 20.11, 1024x832x512 11.38 -> 11.33, 1000x776x548 14.74 -> 14.66,
+// 768^3 15.40 -> 15.33, 1000x777x545 14.72 -> 14.77; after the first one of
+// four 1024^3 took 19.73). The loop written for LATE also changed the larger
+// tiles' schedule with the hook at the top (128x128 +0.6%, the fused gate/up
+// kernel +0.8%), so they keep this one.
+template <int TM, int TN, bool ZERO = true, class Hook = NoHook, bool LATE = false>
 __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, int wn, int lane,
                                      f32x16 (&acc)[TM][TN], Hook hook = {}) {
     using T = Tile<TM, TN>;
@@ -320,14 +327,26 @@ __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, i
                 b[e][j] = bs[krow * T::kBN + (((col >> 2) ^ swz_b(krow)) << 2) + (col & 3)];
             }
         }
-        hook(q);
+        if constexpr (LATE) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+            for (int e = 0; e < 4; ++e) {
+                if (e == 2) hook(q);
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[e][j], acc[i][j], 0, 0, 0);
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[e][j], acc[i][j], 0, 0, 0);
+            }
+        } else {
+            hook(q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][e], b[e][j], acc[i][j], 0, 0, 0);
+        }
     }
 }
 
@@ -443,10 +462,11 @@ __device__ inline void k_loop_dma(const float *__restrict__ A, const float *__re
                     else
                         mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part);
                 } else {
+                    constexpr bool kLate = TM * TN == 1;
                     if (uu == 0)
-                        mma_stage_swz<TM, TN, true>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
+                        mma_stage_swz<TM, TN, true, decltype(spread), kLate>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
                     else
-                        mma_stage_swz<TM, TN, false>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
+                        mma_stage_swz<TM, TN, false, decltype(spread), kLate>(cur, cur + T::kAStageS, wm, wn, lane, part, spread);
                 }
                 if (uu == kFoldStages - 1) {
 #pragma unroll
