@@ -974,7 +974,10 @@ __global__ __launch_bounds__(kThreads * KG) __attribute__((amdgpu_waves_per_eu(K
     // issues the next stage whole at the top of the current one, except with
     // two K groups and for 128x128 tiles, where A at the top and B after
     // quarter 2 measured faster (1000x832x512 12.38 -> 12.26 us, 2500^3
-    // 322.5 -> 314.7); elsewhere that split was 0.5-6% slower.
+    // 322.5 -> 314.7); elsewhere that split was 0.5-6% slower. With the 64x64
+    // tiles' loads after half of each quarter's MFMAs, the four-group 64x64
+    // tiles still lose with B after quarter 1, 2 or 3 (1000x777x513 12.89 ->
+    // 12.93-13.22 us, 1000x777x1027 24.51 -> 25.00-25.87).
     constexpr int kBufQB = KG == 2 || TM * TN == 4 ? 2 : -1;
     if (PATH == kBufAll)
         k_loop_dma<TM, TN, true, -1, 2, true, -1, kBufQB>(A, B, gsmem, N, K, kbegin, nk, m0, n0, wm, wn, lane, t, acc, M, kend);
