@@ -59,7 +59,9 @@ namespace {
 // Halving the barriers (a timing-only copy without the odd stages' barriers)
 // and folding the two waves of a SIMD at different stages (so one
 // wave's MFMAs cover the other's fold) were measured and changed nothing.
-// Also measured and dropped: sixteen waves of 32x32 (four per SIMD), 1%
+// Also measured and dropped: raised wave priority over each stage's matrix
+// work (s_setprio; 4096^3 913.95 -> 915.15 us, 4096x11008x4096 -0.4%);
+// sixteen waves of 32x32 (four per SIMD), 1%
 // slower at every shape; 128x256 tiles of 16-deep stages (eight waves of
 // 32x128: half the operand reads per MFMA), 4096^3 918.5 -> 929 us.
 // Requires M, N multiples of 128, K a multiple of 256 (whole eight-stage
