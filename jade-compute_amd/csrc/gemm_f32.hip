@@ -295,7 +295,8 @@ struct NoHook {
 // 768^3 15.40 -> 15.33, 1000x777x545 14.72 -> 14.77; after the first one of
 // four 1024^3 took 19.73). The loop written for LATE also changed the larger
 // tiles' schedule with the hook at the top (128x128 +0.6%, the fused gate/up
-// kernel +0.8%), so they keep this one.
+// kernel +0.8%), so they keep this one; LATE itself moved 128x64 tiles by
+// 0.15% at most either way (five shapes).
 template <int TM, int TN, bool ZERO = true, class Hook = NoHook, bool LATE = false>
 __device__ inline void mma_stage_swz(const float *as, const float *bs, int wm, int wn, int lane,
                                      f32x16 (&acc)[TM][TN], Hook hook = {}) {
